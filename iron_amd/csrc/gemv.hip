@@ -1,0 +1,566 @@
+// Matrix-vector kernels for batch-1 decode: bf16 GEMV, fused int4-group-32
+// GEMV and the int4 dequantizers.
+//
+// All of them stream the weight matrix from HBM exactly once with 16-byte
+// nontemporal loads. One wavefront owns one (bf16) or R (int4) output rows;
+// each lane walks the row in 16-byte chunks strided by 64 chunks, so one load
+// instruction moves a contiguous 1 KiB per wave. Products accumulate in fp32
+// (v_dot2c_f32_bf16) and the row total is a DPP wave reduction.
+//
+// Each kernel has a fast path, specialised at compile time for the shapes of
+// the Llama decode step (every load issued up front, no bounds checks in the
+// unrolled body), and a generic path for any other valid shape.
+//
+// Optional fusions (used by the decode step, all off for the plain operator):
+//   norm_w   : the input vector is RMS-normalised and scaled by norm_w first
+//              (every wave recomputes sum(x^2); x is a few KiB and L2-resident)
+//   W2       : a second matrix of the same shape; the output is
+//              silu(W.x) * (W2.x)   (the SwiGLU gate/up pair)
+//   residual : added to the (activated) result before the bf16 rounding
+#include "iron_common.hpp"
+#include "../../include/iron_hip.h"
+
+namespace iron {
+namespace {
+
+struct GemvArgs {
+  const uint16_t* W;       // (batches, M, K) bf16
+  const uint16_t* W2;      // optional second (M, K) matrix (SwiGLU up projection)
+  const uint16_t* x;       // (batches, K) bf16
+  uint16_t* y;             // (batches, M) bf16
+  const uint16_t* norm_w;  // optional (K,) RMSNorm weight
+  const uint16_t* resid;   // optional (M,) residual
+  int M, K;
+  float eps;
+  int epi;
+};
+
+// Normalises the 8 bf16 values of an x chunk: bf16(x * inv * w).
+__device__ __forceinline__ uint4 normalize_chunk(uint4 xv, uint4 wv, float inv) {
+  uint4 r;
+  r.x = pack_bf16x2(lo_bf16(xv.x) * inv * lo_bf16(wv.x), hi_bf16(xv.x) * inv * hi_bf16(wv.x));
+  r.y = pack_bf16x2(lo_bf16(xv.y) * inv * lo_bf16(wv.y), hi_bf16(xv.y) * inv * hi_bf16(wv.y));
+  r.z = pack_bf16x2(lo_bf16(xv.z) * inv * lo_bf16(wv.z), hi_bf16(xv.z) * inv * hi_bf16(wv.z));
+  r.w = pack_bf16x2(lo_bf16(xv.w) * inv * lo_bf16(wv.w), hi_bf16(xv.w) * inv * hi_bf16(wv.w));
+  return r;
+}
+
+__device__ __forceinline__ float dot_chunk(uint4 w, uint4 x, float acc) {
+  acc = dot2_bf16(w.x, x.x, acc);
+  acc = dot2_bf16(w.y, x.y, acc);
+  acc = dot2_bf16(w.z, x.z, acc);
+  acc = dot2_bf16(w.w, x.w, acc);
+  return acc;
+}
+
+__device__ __forceinline__ float sumsq_chunk(uint4 v, float acc) {
+  float a;
+  a = lo_bf16(v.x); acc = fmaf(a, a, acc); a = hi_bf16(v.x); acc = fmaf(a, a, acc);
+  a = lo_bf16(v.y); acc = fmaf(a, a, acc); a = hi_bf16(v.y); acc = fmaf(a, a, acc);
+  a = lo_bf16(v.z); acc = fmaf(a, a, acc); a = hi_bf16(v.z); acc = fmaf(a, a, acc);
+  a = lo_bf16(v.w); acc = fmaf(a, a, acc); a = hi_bf16(v.w); acc = fmaf(a, a, acc);
+  return acc;
+}
+
+// inv_rms of a K-vector (K % 8 == 0), computed by one wave (all lanes get it).
+__device__ __forceinline__ float wave_inv_rms(const uint16_t* x, int K, float eps, int lane) {
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  float ss = 0.f;
+  for (int c = lane; c < (K >> 3); c += kWave) ss = sumsq_chunk(xv[c], ss);
+  ss = wave_sum(ss);
+  return rsqrtf(ss / static_cast<float>(K) + eps);
+}
+
+__device__ __forceinline__ void store_row(const GemvArgs& a, size_t idx, int row, float acc, float acc2,
+                                          bool pair) {
+  float v = pair ? silu_f32(acc) * acc2 : apply_epilogue(acc, a.epi);
+  if (a.resid) v += bf16_to_f32(a.resid[row]);
+  a.y[idx] = f32_to_bf16(v);
+}
+
+// Fast path: K == 512*U exactly; each lane holds U chunks of W (and W2) in
+// flight. One wave per output row.
+template <int U, bool PAIR, bool NORM>
+__global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  if (row >= a.M) return;  // uniform per wave; the kernel has no block barrier
+
+  const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
+  const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
+  const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff) + lane;
+  const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) + lane : nullptr;
+  const uint4* xv = reinterpret_cast<const uint4*>(x) + lane;
+
+  uint4 w[U], w2[U], xc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    w[u] = ld_stream16(Wr + u * kWave);
+    if (PAIR) w2[u] = ld_stream16(W2r + u * kWave);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) xc[u] = xv[u * kWave];
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) ss = sumsq_chunk(xc[u], ss);
+    const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w) + lane;
+#pragma unroll
+    for (int u = 0; u < U; ++u) xc[u] = normalize_chunk(xc[u], nw[u * kWave], inv);
+  }
+  float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    acc = dot_chunk(w[u], xc[u], acc);
+    if (PAIR) acc2 = dot_chunk(w2[u], xc[u], acc2);
+  }
+  acc = wave_sum(acc);
+  if (PAIR) acc2 = wave_sum(acc2);
+  if (lane == 0) store_row(a, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
+}
+
+// Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  if (row >= a.M) return;
+  constexpr int U = 4;
+  const int nch = a.K >> 3;
+  const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+  const float inv = a.norm_w ? wave_inv_rms(x, a.K, a.eps, lane) : 1.f;
+  const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
+  const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff);
+  const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) : nullptr;
+  float acc = 0.f, acc2 = 0.f;
+  for (int base = lane; base < nch; base += kWave * U) {
+    uint4 w[U], w2[U], xc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = base + u * kWave;
+      const bool ok = c < nch;
+      w[u] = ok ? ld_stream16(Wr + c) : make_uint4(0, 0, 0, 0);
+      if (PAIR) w2[u] = ok ? ld_stream16(W2r + c) : make_uint4(0, 0, 0, 0);
+      xc[u] = ok ? xv[c] : make_uint4(0, 0, 0, 0);
+      if (ok && a.norm_w) xc[u] = normalize_chunk(xc[u], nw[c], inv);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = dot_chunk(w[u], xc[u], acc);
+      if (PAIR) acc2 = dot_chunk(w2[u], xc[u], acc2);
+    }
+  }
+  acc = wave_sum(acc);
+  if (PAIR) acc2 = wave_sum(acc2);
+  if (lane == 0) store_row(a, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
+}
+
+template <int U, bool PAIR>
+void launch_bf16_fast(const GemvArgs& a, dim3 grid, hipStream_t s) {
+  if (a.norm_w)
+    hipLaunchKernelGGL((gemv_bf16_fast<U, PAIR, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemv_bf16_fast<U, PAIR, false>), grid, dim3(256), 0, s, a);
+}
+
+template <bool PAIR>
+int launch_gemv_bf16(const GemvArgs& a, int batches, hipStream_t s) {
+  dim3 grid((a.M + 3) / 4, batches);
+  const int U = (a.K % 512 == 0) ? a.K / 512 : 0;
+  switch (U) {
+    case 1: launch_bf16_fast<1, PAIR>(a, grid, s); break;
+    case 2: launch_bf16_fast<2, PAIR>(a, grid, s); break;
+    case 4: launch_bf16_fast<4, PAIR>(a, grid, s); break;
+    case 8: launch_bf16_fast<8, PAIR>(a, grid, s); break;
+    case 16:
+      if (!PAIR) {
+        launch_bf16_fast<16, false>(a, grid, s);
+        break;
+      }
+      [[fallthrough]];
+    default: hipLaunchKernelGGL((gemv_bf16_generic<PAIR>), grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("gemv_bf16");
+}
+
+// ---------------------------------------------------------------------------
+// int4, group 32. codes (M, K/2) uint8, two weights per byte along K, low
+// nibble first; scales (M, K/32) bf16. One 16-byte chunk of codes is exactly
+// one group, so lane l owns groups l, l+64, ... of every row it touches.
+//
+// Dequant-free inner product: a nibble n placed in the mantissa of the bf16
+// 0x4300 (=128) gives the exact value 128+n, so one v_bitop3_b32 builds two
+// such weights at once and v_dot2c consumes them. For signed codes the nibble
+// sign bit is flipped in the same op (offset binary, 128+(q+8) = 136+q). The
+// constant part is removed per group with the group's x sum:
+// sum((c+q) x) - c*sum(x). The group scale multiplies the group total once.
+// ---------------------------------------------------------------------------
+struct I4Args {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  const uint8_t* codes2;  // optional SwiGLU up projection
+  const uint16_t* scales2;
+  const uint16_t* x;
+  uint16_t* y;
+  const uint16_t* norm_w;
+  const uint16_t* resid;
+  int M, K;
+  float eps;
+  int epi;
+  uint32_t magic;  // 0x43084308 signed two's-complement nibbles, 0x43004300 unsigned
+  float offset;    // 136 signed, 128 unsigned
+};
+
+// x chunk of one group (32 bf16) rearranged into the nibble-pair order:
+// word q of the codes holds elements 8q..8q+7; the pair extracted at shift 4j
+// is (element 8q+j, element 8q+j+4).
+struct XGroup {
+  uint32_t p[16];
+  float sum;
+};
+
+__device__ __forceinline__ void build_xgroup(const uint4 (&xc)[4], XGroup& g) {
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t w0 = xc[q].x, w1 = xc[q].y, w2 = xc[q].z, w3 = xc[q].w;  // (x0,x1) (x2,x3) (x4,x5) (x6,x7)
+    g.p[q * 4 + 0] = (w0 & 0xffffu) | (w2 << 16);      // (x0, x4)
+    g.p[q * 4 + 1] = (w0 >> 16) | (w2 & 0xffff0000u);  // (x1, x5)
+    g.p[q * 4 + 2] = (w1 & 0xffffu) | (w3 << 16);      // (x2, x6)
+    g.p[q * 4 + 3] = (w1 >> 16) | (w3 & 0xffff0000u);  // (x3, x7)
+    s += lo_bf16(w0) + hi_bf16(w0) + lo_bf16(w1) + hi_bf16(w1) + lo_bf16(w2) + hi_bf16(w2) + lo_bf16(w3) +
+         hi_bf16(w3);
+  }
+  g.sum = s;
+}
+
+// Truth table of f(a, b, c) = (a & b) ^ c for v_bitop3_b32 (inputs 0xF0, 0xCC, 0xAA).
+constexpr unsigned kAndXor = (0xF0u & 0xCCu) ^ 0xAAu;
+
+// `magic` = 0x43084308 for signed codes (mask, then XOR sets the 0x4300
+// exponent bits and flips the nibble sign bit: 128 + (q + 8)), 0x43004300 for
+// unsigned codes (128 + n). One v_bitop3_b32 + one v_dot2c per weight pair.
+__device__ __forceinline__ float i4_group_dot(uint4 c, const XGroup& g, uint32_t magic) {
+  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
+  float acc = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t u = words[q];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wpair = __builtin_amdgcn_bitop3_b32(u >> (4 * j), 0x000f000fu, magic, kAndXor);
+      acc = dot2_bf16(wpair, g.p[q * 4 + j], acc);
+    }
+  }
+  return acc;
+}
+
+__device__ __forceinline__ void store_i4_row(const I4Args& a, int row, float t, float t2, bool pair) {
+  float v = pair ? silu_f32(t) * t2 : apply_epilogue(t, a.epi);
+  if (a.resid) v += bf16_to_f32(a.resid[row]);
+  a.y[row] = f32_to_bf16(v);
+}
+
+// Fast path: K == 2048*GPL (every lane owns exactly GPL groups of a row) and
+// M % R == 0 (R rows per wave, sharing the x preparation).
+template <int GPL, int R, bool PAIR, bool NORM>
+__global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (row0 >= a.M) return;  // uniform per wave
+  constexpr int G = GPL * kWave;
+  constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
+
+  // Weight loads first, so they are in flight while x is prepared.
+  uint4 cw[R][GPL], cw2[R][GPL];
+  uint16_t sc[R][GPL], sc2[R][GPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const size_t row = static_cast<size_t>(row0 + r);
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const int g = lane + j * kWave;
+      cw[r][j] = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
+      sc[r][j] = a.scales[row * G + g];
+      if (PAIR) {
+        cw2[r][j] = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
+        sc2[r][j] = a.scales2[row * G + g];
+      }
+    }
+  }
+
+  uint4 xr[GPL][4];
+  const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+#pragma unroll
+  for (int j = 0; j < GPL; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xr[j][q] = xv[(lane + j * kWave) * 4 + q];
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < GPL; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[j][q], ss);
+    const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+#pragma unroll
+    for (int j = 0; j < GPL; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xr[j][q] = normalize_chunk(xr[j][q], nw[(lane + j * kWave) * 4 + q], inv);
+  }
+  XGroup xg[GPL];
+#pragma unroll
+  for (int j = 0; j < GPL; ++j) build_xgroup(xr[j], xg[j]);
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f, acc2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const float d = i4_group_dot(cw[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+      acc = fmaf(bf16_to_f32(sc[r][j]), d, acc);
+      if (PAIR) {
+        const float d2 = i4_group_dot(cw2[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+        acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
+      }
+    }
+    const float t = wave_sum(acc);
+    const float t2 = PAIR ? wave_sum(acc2) : 0.f;
+    if (lane == 0) store_i4_row(a, row0 + r, t, t2, PAIR);
+  }
+}
+
+// Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const int G = a.K >> 5;
+  const size_t crow = static_cast<size_t>(a.K) >> 1;
+  const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+  const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+  const float inv = a.norm_w ? wave_inv_rms(a.x, a.K, a.eps, lane) : 1.f;
+  float acc = 0.f, acc2 = 0.f;
+  for (int g = lane; g < G; g += kWave) {
+    const uint4 c = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
+    const float s = bf16_to_f32(a.scales[static_cast<size_t>(row) * G + g]);
+    uint4 c2 = make_uint4(0, 0, 0, 0);
+    float s2 = 0.f;
+    if (PAIR) {
+      c2 = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
+      s2 = bf16_to_f32(a.scales2[static_cast<size_t>(row) * G + g]);
+    }
+    uint4 xc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xc[q] = xv[g * 4 + q];
+      if (a.norm_w) xc[q] = normalize_chunk(xc[q], nw[g * 4 + q], inv);
+    }
+    XGroup t;
+    build_xgroup(xc, t);
+    acc = fmaf(s, i4_group_dot(c, t, a.magic) - a.offset * t.sum, acc);
+    if (PAIR) acc2 = fmaf(s2, i4_group_dot(c2, t, a.magic) - a.offset * t.sum, acc2);
+  }
+  const float t = wave_sum(acc);
+  const float t2 = PAIR ? wave_sum(acc2) : 0.f;
+  if (lane == 0) store_i4_row(a, row, t, t2, PAIR);
+}
+
+template <int GPL, int R, bool PAIR>
+void launch_i4_fast(const I4Args& a, hipStream_t s) {
+  dim3 grid((a.M / R + 3) / 4), block(256);
+  if (a.norm_w)
+    hipLaunchKernelGGL((gemv_i4_fast<GPL, R, PAIR, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((gemv_i4_fast<GPL, R, PAIR, false>), grid, block, 0, s, a);
+}
+
+template <bool PAIR>
+int launch_gemv_i4(const I4Args& a, hipStream_t s) {
+  const int gpl = (a.K % 2048 == 0) ? a.K / 2048 : 0;
+  // Two rows per wave when there are enough rows to keep >= 4 waves per SIMD.
+  const bool r2 = !PAIR && a.M % 2 == 0 && a.M >= 8192;
+  switch (gpl) {
+    case 1:
+      if (r2) launch_i4_fast<1, 2, PAIR>(a, s);
+      else launch_i4_fast<1, 1, PAIR>(a, s);
+      break;
+    case 2: launch_i4_fast<2, 1, PAIR>(a, s); break;
+    case 4: launch_i4_fast<4, 1, PAIR>(a, s); break;
+    default: hipLaunchKernelGGL((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a); break;
+  }
+  return check_launch("gemv_i4g32");
+}
+
+// ---------------------------------------------------------------------------
+// Dequantizers (bit-exact: bf16_rne(float(q) * float(scale))).
+// ---------------------------------------------------------------------------
+
+// Planar: codes (N, K/2), scales (N, K/group). One thread = 8 consecutive
+// weights (4 code bytes -> one 16-byte store).
+__global__ __launch_bounds__(256) void dequant_planar_kernel(const uint8_t* __restrict__ codes,
+                                                             const uint16_t* __restrict__ scales,
+                                                             uint16_t* __restrict__ out, int N, int K,
+                                                             int group, int is_signed) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const size_t per_row = static_cast<size_t>(K) >> 3;
+  if (t >= per_row * static_cast<size_t>(N)) return;
+  const size_t row = t / per_row;
+  const int k0 = static_cast<int>(t - row * per_row) * 8;
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(codes + row * (K >> 1) + (k0 >> 1));
+  const int G = K / group;
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float v[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int n = (w >> (4 * (e + h))) & 0xf;
+      const int q = is_signed ? ((n ^ 8) - 8) : n;
+      const float s = bf16_to_f32(scales[row * G + (k0 + e + h) / group]);
+      v[h] = static_cast<float>(q) * s;
+    }
+    o[e >> 1] = pack_bf16x2(v[0], v[1]);
+  }
+  *reinterpret_cast<uint4*>(out + row * K + k0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Tile payload: per tile, tile/2 code bytes then tile/group bf16 scales
+// (little-endian bytes). One thread = 2 weights (one code byte).
+__global__ __launch_bounds__(256) void dequant_payload_kernel(const uint8_t* __restrict__ payload,
+                                                              uint16_t* __restrict__ out, long long size,
+                                                              int tile, int group, int is_signed) {
+  const long long t = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const long long e0 = t * 2;
+  if (e0 >= size) return;
+  const long long tile_idx = e0 / tile;
+  const int in_tile = static_cast<int>(e0 - tile_idx * tile);
+  const long long tile_bytes = tile / 2 + 2LL * (tile / group);
+  const uint8_t* base = payload + tile_idx * tile_bytes;
+  const uint8_t byte = base[in_tile >> 1];
+  const int sidx = in_tile / group;  // both weights of a byte share a group (group is even)
+  const uint8_t* sp = base + tile / 2 + 2 * sidx;
+  const float s = bf16_to_f32(static_cast<uint16_t>(sp[0] | (sp[1] << 8)));
+  const int n0 = byte & 0xf, n1 = byte >> 4;
+  const int q0 = is_signed ? ((n0 ^ 8) - 8) : n0;
+  const int q1 = is_signed ? ((n1 ^ 8) - 8) : n1;
+  out[e0] = f32_to_bf16(static_cast<float>(q0) * s);
+  out[e0 + 1] = f32_to_bf16(static_cast<float>(q1) * s);
+}
+
+}  // namespace
+}  // namespace iron
+
+using namespace iron;
+
+extern "C" int iron_gemv_bf16(const void* W, const void* x, void* y, int M, int K, int batches,
+                              int epilogue, void* stream) {
+  IRON_REQUIRE(W && x && y, "iron_gemv_bf16: null pointer");
+  IRON_REQUIRE(M > 0 && K > 0 && batches > 0, "iron_gemv_bf16: M=%d K=%d batches=%d must be positive", M,
+               K, batches);
+  IRON_REQUIRE(K % 8 == 0, "iron_gemv_bf16: K=%d must be a multiple of 8", K);
+  IRON_REQUIRE(aligned16(W) && aligned16(x), "iron_gemv_bf16: W and x must be 16-byte aligned");
+  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16: bad epilogue %d",
+               epilogue);
+  GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x),
+             static_cast<uint16_t*>(y), nullptr, nullptr, M, K, 0.f, epilogue};
+  return launch_gemv_bf16<false>(a, batches, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x, void* y, int M, int K,
+                                    const void* norm_w, float eps, const void* residual, int epilogue,
+                                    void* stream) {
+  IRON_REQUIRE(W && x && y, "iron_gemv_bf16_fused: null pointer");
+  IRON_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "iron_gemv_bf16_fused: M=%d K=%d (K must be a multiple of 8)",
+               M, K);
+  IRON_REQUIRE(aligned16(W) && aligned16(x) && (!W2 || aligned16(W2)) && (!norm_w || aligned16(norm_w)),
+               "iron_gemv_bf16_fused: operands must be 16-byte aligned");
+  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16_fused: bad epilogue %d",
+               epilogue);
+  IRON_REQUIRE(!(W2 && epilogue != EPI_NONE), "iron_gemv_bf16_fused: the SwiGLU pair takes no epilogue");
+  IRON_REQUIRE(y != x, "iron_gemv_bf16_fused: y must not alias x");
+  GemvArgs a{static_cast<const uint16_t*>(W),      static_cast<const uint16_t*>(W2),
+             static_cast<const uint16_t*>(x),      static_cast<uint16_t*>(y),
+             static_cast<const uint16_t*>(norm_w), static_cast<const uint16_t*>(residual),
+             M,                                    K,
+             eps,                                  epilogue};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return W2 ? launch_gemv_bf16<true>(a, 1, s) : launch_gemv_bf16<false>(a, 1, s);
+}
+
+extern "C" int iron_gemv_i4g32(const void* codes, const void* scales, const void* x, void* y, int M, int K,
+                               int is_signed, void* stream) {
+  return iron_gemv_i4g32_fused(codes, scales, nullptr, nullptr, x, y, M, K, is_signed, nullptr, 0.f, nullptr,
+                               0, stream);
+}
+
+extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, const void* codes2,
+                                     const void* scales2, const void* x, void* y, int M, int K, int is_signed,
+                                     const void* norm_w, float eps, const void* residual, int epilogue,
+                                     void* stream) {
+  IRON_REQUIRE(codes && scales && x && y, "iron_gemv_i4g32: null pointer");
+  IRON_REQUIRE((codes2 == nullptr) == (scales2 == nullptr), "iron_gemv_i4g32: codes2/scales2 come together");
+  IRON_REQUIRE(M > 0 && K > 0 && K % 32 == 0, "iron_gemv_i4g32: M=%d K=%d (K must be a multiple of 32)", M,
+               K);
+  IRON_REQUIRE(aligned16(codes) && aligned16(x) && (!codes2 || aligned16(codes2)) &&
+                   (!norm_w || aligned16(norm_w)),
+               "iron_gemv_i4g32: codes, x and norm weight must be 16-byte aligned");
+  IRON_REQUIRE((reinterpret_cast<uintptr_t>(scales) & 1u) == 0, "iron_gemv_i4g32: scales must be 2-byte aligned");
+  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_i4g32: bad epilogue %d",
+               epilogue);
+  IRON_REQUIRE(!(codes2 && epilogue != EPI_NONE), "iron_gemv_i4g32: the SwiGLU pair takes no epilogue");
+  IRON_REQUIRE(y != x, "iron_gemv_i4g32: y must not alias x");
+  I4Args a{static_cast<const uint8_t*>(codes),
+           static_cast<const uint16_t*>(scales),
+           static_cast<const uint8_t*>(codes2),
+           static_cast<const uint16_t*>(scales2),
+           static_cast<const uint16_t*>(x),
+           static_cast<uint16_t*>(y),
+           static_cast<const uint16_t*>(norm_w),
+           static_cast<const uint16_t*>(residual),
+           M,
+           K,
+           eps,
+           epilogue,
+           is_signed ? 0x43084308u : 0x43004300u,
+           is_signed ? 136.f : 128.f};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return codes2 ? launch_gemv_i4<true>(a, s) : launch_gemv_i4<false>(a, s);
+}
+
+extern "C" int iron_dequant_i4(const void* codes, const void* scales, void* out, int N, int K, int group,
+                               int is_signed, void* stream) {
+  IRON_REQUIRE(codes && scales && out, "iron_dequant_i4: null pointer");
+  IRON_REQUIRE(N > 0 && K > 0 && K % 8 == 0, "iron_dequant_i4: N=%d K=%d (K must be a multiple of 8)", N, K);
+  IRON_REQUIRE(group > 0 && group % 2 == 0 && K % group == 0,
+               "iron_dequant_i4: group=%d must be even and divide K=%d", group, K);
+  IRON_REQUIRE(aligned16(out) && (reinterpret_cast<uintptr_t>(codes) & 3u) == 0,
+               "iron_dequant_i4: out must be 16-byte and codes 4-byte aligned");
+  const size_t threads = static_cast<size_t>(N) * (K / 8);
+  hipLaunchKernelGGL(dequant_planar_kernel, dim3((threads + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(codes),
+                     static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(out), N, K, group, is_signed);
+  return check_launch("dequant_i4");
+}
+
+extern "C" int iron_dequant_i4_payload(const void* payload, void* out, long long size, int tile_size,
+                                       int group_size, int is_signed, void* stream) {
+  IRON_REQUIRE(payload && out, "iron_dequant_i4_payload: null pointer");
+  IRON_REQUIRE(size > 0 && tile_size > 0 && group_size > 0, "iron_dequant_i4_payload: sizes must be positive");
+  IRON_REQUIRE(size % tile_size == 0, "iron_dequant_i4_payload: size %lld must be a multiple of tile_size %d",
+               size, tile_size);
+  IRON_REQUIRE(tile_size % group_size == 0 && group_size % 2 == 0,
+               "iron_dequant_i4_payload: group_size %d must be even and divide tile_size %d", group_size,
+               tile_size);
+  const long long threads = size / 2;
+  hipLaunchKernelGGL(dequant_payload_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(payload),
+                     static_cast<uint16_t*>(out), size, tile_size, group_size, is_signed);
+  return check_launch("dequant_i4_payload");
+}

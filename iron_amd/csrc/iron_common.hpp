@@ -1,0 +1,139 @@
+// Shared device helpers for the gfx950 kernels of libiron_hip.
+//
+// bf16 values travel as raw uint16 bit patterns so that every rounding step is
+// explicit: widening is a 16-bit shift, narrowing is round-to-nearest-even
+// written out below (torch's CPU bf16 conversion rounds the same way, which is
+// what makes the int4 dequant bit-exact against the test oracle).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace iron {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;  // CDNA4 wavefront width
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even narrowing; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Low / high bf16 of a packed 32-bit word, widened to fp32.
+__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi with fp32 accumulation (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+// v + (v moved across lanes by DPP control CTRL); lanes outside ROWMASK add 0.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float add_dpp(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                    ROWMASK, 0xf, false));
+}
+
+// Full-wave sum with DPP row operations (no LDS round trip): pairs, quads,
+// half-row mirror, row mirror, then row_bcast:15 / row_bcast:31 fold the four
+// 16-lane rows into lane 63, which is broadcast through an SGPR. Every lane
+// returns the total. All 64 lanes must be active.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = add_dpp<0xB1>(v);        // quad_perm [1,0,3,2]
+  v = add_dpp<0x4E>(v);        // quad_perm [2,3,0,1]
+  v = add_dpp<0x141>(v);       // row_half_mirror
+  v = add_dpp<0x140>(v);       // row_mirror: every lane holds its row's sum
+  v = add_dpp<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = add_dpp<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float max_dpp(float v) {
+  // lanes outside ROWMASK keep `old` = -inf, so the max leaves them unchanged
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                      static_cast<int>(0xff800000u), __builtin_bit_cast(int, v), CTRL, ROWMASK, 0xf, false)));
+}
+
+// Full-wave max, same DPP pattern as wave_sum. All 64 lanes must be active.
+__device__ __forceinline__ float wave_max(float v) {
+  v = max_dpp<0xB1>(v);
+  v = max_dpp<0x4E>(v);
+  v = max_dpp<0x141>(v);
+  v = max_dpp<0x140>(v);
+  v = max_dpp<0x142, 0xA>(v);
+  v = max_dpp<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Streaming 16-byte load that bypasses cache retention (weights are read once).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_stream16(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), tanh via exp.
+  const float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
+  const float t = 1.0f - 2.0f / (1.0f + __expf(2.0f * inner));
+  return 0.5f * x * (1.0f + t);
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Epilogue selectors shared by GEMV and GEMM entry points.
+enum Epilogue : int { EPI_NONE = 0, EPI_GELU_TANH = 1, EPI_SILU = 2, EPI_SIGMOID = 3, EPI_GELU_SIGMOID = 4 };
+
+__device__ __forceinline__ float apply_epilogue(float v, int epi) {
+  switch (epi) {
+    case EPI_GELU_TANH: return gelu_tanh_f32(v);
+    case EPI_SILU: return v * sigmoid_f32(v);
+    case EPI_SIGMOID: return sigmoid_f32(v);
+    case EPI_GELU_SIGMOID: return v * sigmoid_f32(1.702f * v);
+    default: return v;
+  }
+}
+
+}  // namespace iron
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing shared by every entry point.
+// ---------------------------------------------------------------------------
+namespace iron {
+void set_error(const char* fmt, ...);
+int fail_einval(const char* fmt, ...);
+int check_launch(const char* what);
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace iron
+
+#define IRON_EINVAL 22
+#define IRON_REQUIRE(cond, ...)                         \
+  do {                                                  \
+    if (!(cond)) return ::iron::fail_einval(__VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,31 @@
+"""The operator library (catalog of iron/operators/__init__.py:13-47).
+
+Operators are re-exported lazily (PEP 562):
+
+    from iron_amd.operators import GEMV   # imports iron_amd.operators.gemv.op only
+"""
+
+import importlib
+
+_OPERATOR_MODULES = {
+    "Dequant": "dequant",
+    "GEMV": "gemv",
+    "GEMVInt4": "gemv_int4",
+}
+
+_SUBPACKAGES: tuple = ()
+
+__all__ = sorted(set(_OPERATOR_MODULES) | set(_SUBPACKAGES))
+
+
+def __getattr__(name):
+    if name in _SUBPACKAGES:
+        return importlib.import_module(f".{name}", __name__)
+    module = _OPERATOR_MODULES.get(name)
+    if module is None:
+        raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
+    return getattr(importlib.import_module(f".{module}.op", __name__), name)
+
+
+def __dir__():
+    return sorted(set(globals()) | set(_OPERATOR_MODULES) | set(_SUBPACKAGES))

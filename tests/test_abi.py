@@ -1,0 +1,51 @@
+"""The C ABI: the library loads and exports exactly what include/iron_hip.h declares."""
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "iron_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(iron_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "iron_gemv_bf16" in names and "iron_last_error" in names
+    assert len(names) >= 8
+
+
+def test_library_exports_every_declared_symbol():
+    from iron_amd import _lib
+
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True)
+    exported = set(re.findall(r"\bT (iron_\w+)", out.stdout))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    for n in declared_functions():
+        assert hasattr(lib, n)
+
+
+def test_binding_covers_header():
+    from iron_amd import _lib
+
+    assert sorted(_lib.exported_symbols()) == declared_functions()
+
+
+def test_abi_version_and_error_path():
+    from iron_amd import _lib
+
+    lib = _lib.load()
+    assert lib.iron_abi_version() == 1
+    with pytest.raises(_lib.IronHipError, match="null pointer"):
+        _lib.call("iron_gemv_bf16", None, None, None, 16, 16, 1, 0, None)
+    with pytest.raises(_lib.IronHipError, match="multiple of 8"):
+        _lib.call("iron_gemv_bf16", 16, 16, 16, 16, 12, 1, 0, None)
