@@ -88,6 +88,87 @@ int iron_dequant_i4(const void* codes, const void* scales, void* out, int N, int
 int iron_dequant_i4_payload(const void* payload, void* out, long long size, int tile_size, int group_size,
                             int is_signed, void* stream);
 
+/* ------------------------------------------------ Norm and elementwise ---- */
+
+/* Row-wise RMSNorm over `cols` (cols % 8 == 0, cols <= 16384):
+ *   s = x (+ residual, rounded to bf16); sum_out = s when non-NULL;
+ *   out = s * rsqrt(mean(s^2) + eps) [* w]          (w NULL = unweighted)
+ * fp32 math, one bf16 rounding. out may alias x; sum_out may alias x.
+ * Replaces RMSNorm.get_callable() -> (input, [weight,] output):
+ * iron/operators/rms_norm/op.py:19-122, reference rms_norm/reference.py:7-16;
+ * with residual it also absorbs ElementwiseAdd (elementwise_add/op.py:12-24). */
+int iron_rmsnorm(const void* x, const void* residual, const void* w, void* out, void* sum_out, int rows, int cols,
+                 float eps, void* stream);
+
+/* out = a + b, a * b over n bf16 (16-byte aligned). out may alias a or b.
+ * Replace ElementwiseAdd / ElementwiseMul.get_callable() -> (a, b, out):
+ * iron/operators/elementwise_add/op.py:12-24, elementwise_mul/op.py:12-24. */
+int iron_add(const void* a, const void* b, void* out, long long n, void* stream);
+int iron_mul(const void* a, const void* b, void* out, long long n, void* stream);
+
+/* out = silu(x). Replaces SiLU.get_callable() -> (input, output):
+ * iron/operators/silu/op.py:12-26. */
+int iron_silu(const void* x, void* out, long long n, void* stream);
+
+/* out = silu(gate) * up: the SiLU -> ElementwiseMul pair of
+ * iron/operators/swiglu_decode/op.py:58-59 in one pass. */
+int iron_silu_mul(const void* gate, const void* up, void* out, long long n, void* stream);
+
+/* out = gelu_tanh(x) (iron/operators/gelu/reference.py semantics). */
+int iron_gelu(const void* x, void* out, long long n, void* stream);
+
+/* Row softmax over cols (cols % 8 == 0, cols <= 16384) in fp32; columns >=
+ * valid_cols are masked to -inf (output 0). valid_cols_dev (device int32,
+ * may be NULL) overrides valid_cols at run time (graph-capturable).
+ * Replaces Softmax.get_callable() -> (input, output) with its runtime
+ * vector-size mask: iron/operators/softmax/op.py:21-97, design.py:74-91. */
+int iron_softmax(const void* x, void* out, int rows, int cols, int valid_cols, const int* valid_cols_dev,
+                 void* stream);
+
+/* RoPE from a packed angle table (angle_rows, cols) of interleaved [cos, sin]
+ * pairs (bf16, or fp32 when angles_fp32); row r uses angle row
+ * r / (rows / angle_rows). method 0 rotates the two halves, 1 interleaved
+ * pairs. fp32 math, one bf16 rounding; out may alias x.
+ * Replaces RoPE.get_callable() -> (input, angles, output):
+ * iron/operators/rope/op.py:18-92, reference rope/reference.py:69-102. */
+int iron_rope(const void* x, const void* angles, int angles_fp32, void* out, int rows, int cols, int angle_rows,
+              int method, void* stream);
+
+/* ----------------------------------------------------------- Attention ---- */
+
+/* Bytes of workspace iron_gqa_decode needs for this shape (-1 if invalid).
+ * The first 256 bytes are ticket counters: zero them once after allocation;
+ * every call leaves them zero again. */
+long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
+
+/* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}):
+ *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
+ *                                               (angle_rows, 64) [cos,sin])
+ *   k_cache[:, pos] = k', v_cache[:, pos] = v_new
+ *   out[h] = softmax(scale * q'[h] . K[h/G, 0..pos]) V[h/G, 0..pos]  (fp32)
+ * q (H,64), k_new/v_new (Hkv,64), caches (Hkv,max_len,64), out (H,64) bf16.
+ * pos_dev (device int32, may be NULL) overrides pos at run time.
+ * Replaces the decode attention runlist (RoPE, StridedCopy, Repeat, GEMV
+ * scores, scale Mul, masked Softmax, Transpose, GEMV context) of
+ * iron/applications/llama_3.2_1b/llama_npu.py:486-523 and the CPU golden
+ * llama_cpu.py:49-148. */
+int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                    const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
+                    int head_dim, int max_len, int pos, const int* pos_dev, float scale, void* stream);
+
+/* Flash attention over strided Q (H,Sq,64), K/V (Hkv,Skv,64), out (H,Sq,64)
+ * (element strides per head and per row; rows 16-byte aligned). Query row i
+ * sits at position q_offset+i; with causal it sees keys <= that position.
+ * fp32 online softmax. Rows [Sq, out_rows) of out are written as zeros (the
+ * MHA operator's padded layout); pass out_rows <= Sq for none. Replaces MHA.get_callable() -> (Q, K, V, O):
+ * iron/operators/mha/op.py:21-135, golden mha/reference.py:27-94, and the
+ * CPU prefill attention of llama_npu.py:948-990. */
+int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads, int n_kv_heads,
+                           int seq_q, int seq_kv, int head_dim, long long q_head_stride, long long q_row_stride,
+                           long long kv_head_stride, long long kv_row_stride, long long o_head_stride,
+                           long long o_row_stride, int out_rows, int causal, int q_offset, float scale,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 _LL = ctypes.c_longlong
 
-# name -> argtypes. Every function returns int (0 = success).
+# name -> argtypes (every function returns int, 0 = success) ...
 SIGNATURES: dict[str, list] = {
     "iron_gemv_bf16": [_P, _P, _P, _I, _I, _I, _I, _P],
     "iron_gemv_bf16_fused": [_P, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P],
@@ -30,6 +30,21 @@ SIGNATURES: dict[str, list] = {
     "iron_gemv_i4g32_fused": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _F, _P, _I, _P],
     "iron_dequant_i4": [_P, _P, _P, _I, _I, _I, _I, _P],
     "iron_dequant_i4_payload": [_P, _P, _LL, _I, _I, _I, _P],
+    "iron_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
+    "iron_add": [_P, _P, _P, _LL, _P],
+    "iron_mul": [_P, _P, _P, _LL, _P],
+    "iron_silu": [_P, _P, _LL, _P],
+    "iron_silu_mul": [_P, _P, _P, _LL, _P],
+    "iron_gelu": [_P, _P, _LL, _P],
+    "iron_softmax": [_P, _P, _I, _I, _I, _P, _P],
+    "iron_rope": [_P, _P, _I, _P, _I, _I, _I, _I, _P],
+    "iron_gqa_decode": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P],
+    "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
+}
+
+# ... except these queries, which return a value.
+QUERIES: dict[str, tuple] = {
+    "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
 }
 
 _lock = threading.Lock()
@@ -64,13 +79,17 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)  # AttributeError if the build lacks it
             fn.restype = _I
             fn.argtypes = argtypes
+        for name, (restype, argtypes) in QUERIES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
         _lib = lib
         return lib
 
 
 def exported_symbols() -> list[str]:
     """Names of the C entry points this binding declares (for export checks)."""
-    return ["iron_last_error", "iron_abi_version", *SIGNATURES]
+    return ["iron_last_error", "iron_abi_version", *SIGNATURES, *QUERIES]
 
 
 def call(name: str, *args) -> None:
@@ -80,6 +99,11 @@ def call(name: str, *args) -> None:
     if rc != 0:
         msg = lib.iron_last_error().decode(errors="replace")
         raise IronHipError(f"{name} failed (code {rc}): {msg}")
+
+
+def query(name: str, *args):
+    """Call a value-returning entry point (see QUERIES)."""
+    return getattr(load(), name)(*args)
 
 
 def ptr(t) -> int | None:

@@ -121,6 +121,8 @@ class HIPOperator(AIEOperatorBase):
     torch's current stream of the tensors' device.
     """
 
+    # argument index -> dtypes accepted besides the spec's own
+    _extra_dtypes: ClassVar[dict] = {}
     _name_aliases: ClassVar[dict[str, str]] = {
         "num_aie_columns": "c",
         "num_channels": "ch",
@@ -168,7 +170,7 @@ class HIPOperator(AIEOperatorBase):
                 dev = t.device
             elif t.device != dev:
                 raise ValueError(f"argument {i} is on {t.device}, expected {dev}")
-            if t.dtype != spec.dtype:
+            if t.dtype != spec.dtype and t.dtype not in self._extra_dtypes.get(i, ()):
                 raise ValueError(
                     f"argument {i} of {type(self).__name__} has dtype {t.dtype}, expected {spec.dtype}"
                 )

@@ -9,8 +9,16 @@ import importlib
 
 _OPERATOR_MODULES = {
     "Dequant": "dequant",
+    "ElementwiseAdd": "elementwise_add",
+    "ElementwiseMul": "elementwise_mul",
     "GEMV": "gemv",
     "GEMVInt4": "gemv_int4",
+    "GQADecode": "gqa_decode",
+    "MHA": "mha",
+    "RMSNorm": "rms_norm",
+    "RoPE": "rope",
+    "SiLU": "silu",
+    "Softmax": "softmax",
 }
 
 _SUBPACKAGES: tuple = ()

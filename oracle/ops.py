@@ -466,7 +466,7 @@ def verify_buffer(output, reference, rel_tol=0.04, abs_tol=1e-6, max_error_rate=
     b = reference.detach().float().cpu().reshape(-1)[: a.numel()]
     diff = (a - b).abs()
     tol = torch.maximum(torch.full_like(diff, abs_tol), rel_tol * (a.abs() + b.abs()))
-    bad = ~(diff < tol)
+    bad = ~((diff < tol) | (a == b))
     bad &= ~(torch.isnan(a) & torch.isnan(b))
     n_bad = int(bad.sum())
     if n_bad == 0 or n_bad <= max_error_rate * a.numel():

@@ -1,0 +1,104 @@
+"""GPU parity: GQA decode (split-K flash-decode) and MHA prefill against the oracle.
+
+BASELINE config 3 (32 q-heads, 8 KV heads, d 64, KV length 2048, RoPE llama3
+theta 500000 at position 2047, scale 1/8, fp32 softmax) at full size, plus
+positions on and around the 64-position chunk edges, the first token and the
+last cache slot. MHA follows the reference test list (mha/test.py:13-31) and
+tolerance (rel 4e-2 / abs 0.15, 0.5% mismatches allowed).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import configs, ops
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+
+
+def _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, pos_tensor=False):
+    from iron_amd.operators import GQADecode
+
+    H, Hkv = q.shape[0], kn.shape[0]
+    op = GQADecode(num_heads=H, num_kv_heads=Hkv, head_dim=64, max_len=max_len, angle_rows=angles.shape[0])
+    kcd = torch.zeros(Hkv, max_len, 64, dtype=BF16, device=gpu)
+    vcd = torch.zeros(Hkv, max_len, 64, dtype=BF16, device=gpu)
+    kcd[:, :pos] = kc[:, :pos].to(gpu)
+    vcd[:, :pos] = vc[:, :pos].to(gpu)
+    out = torch.empty(H, 64, dtype=BF16, device=gpu)
+    if pos_tensor:
+        op.position_tensor = torch.tensor([pos], dtype=torch.int32, device=gpu)
+    else:
+        op.set_position(pos)
+    fn = op.get_callable()
+    fn(q.to(gpu), kn.to(gpu), vn.to(gpu), kcd, vcd, angles.to(gpu), out)
+    torch.cuda.synchronize()
+    return out.cpu(), kcd.cpu(), vcd.cpu(), op
+
+
+def test_config3_gqa_decode(gpu):
+    q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode()
+    ref, kref, vref = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    out, kcd, vcd, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=2048)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+    # the new key (rotated) and value are appended at pos, bit-exact
+    assert torch.equal(kcd[:, pos], kref[:, pos]) and torch.equal(vcd[:, pos], vref[:, pos])
+
+
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 127, 1000, 4095])
+@pytest.mark.parametrize("use_tensor", [False, True])
+def test_gqa_decode_positions(gpu, pos, use_tensor):
+    max_len = 4096
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(L=max_len, seed=pos + 1)
+    angles = ops.rope_angles_table(64, max_len)
+    ref, kref, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    out, kcd, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, pos_tensor=use_tensor)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (pos, max_abs, rel_l2)
+    assert torch.equal(kcd[:, pos], kref[:, pos])
+
+
+@pytest.mark.parametrize("H,Hkv", [(32, 32), (32, 16), (16, 2)])
+def test_gqa_decode_group_sizes(gpu, H, Hkv):
+    q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, L=300, seed=3)
+    ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    out, _, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2
+
+
+def test_gqa_decode_workspace_reuse(gpu):
+    """The ticket counters reset themselves: repeated calls on one workspace stay correct."""
+    q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(L=512, seed=11)
+    ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    out, _, _, op = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
+    ws = op.workspace(torch.device(gpu))
+    assert int(ws[:256].view(torch.int32).abs().sum()) == 0
+    for _ in range(3):
+        out2, _, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
+        assert torch.equal(out2, out)
+    assert ops.max_abs_rel_l2(out, ref)[0] <= 2e-2
+
+
+@pytest.mark.parametrize(
+    "seq_len,heads,kv",
+    [(16384, 1, 0), (2048, 8, 2), (1000, 4, 4), (64, 2, 1), (100, 32, 8), (512, 32, 8)],
+)
+def test_mha_causal(gpu, seq_len, heads, kv):
+    from iron_amd.operators import MHA
+
+    g = ops.mha_golden(heads=heads, S_q=seq_len, S_kv=seq_len, d=64, num_kv_heads=kv)
+    op = MHA(num_heads=heads, seq_len=seq_len, d=64, num_KV_heads=kv)
+    sp = op.seq_padded
+    pad = lambda t: torch.nn.functional.pad(t, (0, 0, 0, sp - seq_len))
+    Q, K, V = pad(g["Q"]), pad(g["K"]), pad(g["V"])
+    O = torch.empty(Q.numel(), dtype=BF16, device=gpu)
+    op.get_callable()(Q.to(gpu).flatten(), K.to(gpu).flatten(), V.to(gpu).flatten(), O)
+    torch.cuda.synchronize()
+    ref = pad(g["O"])
+    errs = ops.verify_buffer(O, ref, rel_tol=4e-2, abs_tol=1.5e-1, max_error_rate=0.005)
+    assert not errs, f"{len(errs)} mismatches"
+    assert torch.all(O.view(heads, sp, 64)[:, seq_len:].cpu() == 0)
