@@ -88,6 +88,13 @@ int iron_dequant_i4(const void* codes, const void* scales, void* out, int N, int
 int iron_dequant_i4_payload(const void* payload, void* out, long long size, int tile_size, int group_size,
                             int is_signed, void* stream);
 
+/* Symmetric int4 group-32 quantiser for weight preparation: per 32 weights
+ * along K, scale = bf16(max|w| / 7), q = clamp(rint(w / scale), -8, 7); writes
+ * codes (N,K/2) (signed, low nibble first) and scales (N,K/32). Produces the
+ * format iron_gemv_i4g32 and iron_dequant_i4 consume (no reference
+ * counterpart: the reference ships pre-quantized payloads). */
+int iron_quantize_i4g32(const void* W, void* codes, void* scales, int N, int K, void* stream);
+
 /* ------------------------------------------------ Norm and elementwise ---- */
 
 /* Row-wise RMSNorm over `cols` (cols % 8 == 0, cols <= 16384):
@@ -168,6 +175,46 @@ int iron_attention_prefill(const void* q, const void* k, const void* v, void* ou
                            long long kv_head_stride, long long kv_row_stride, long long o_head_stride,
                            long long o_row_stride, int out_rows, int causal, int q_offset, float scale,
                            void* stream);
+
+/* ---------------------------------------------------------------- GEMM ---- */
+
+/* C = clamp(act(bf16(A . B^T))) on bf16 MFMA, fp32 accumulation:
+ * A (M,K), B (N,K) both K-contiguous (K % 64 == 0, 16-byte aligned), C (M,N)
+ * with row stride ldc. epilogue: enum iron_epilogue (applied after the bf16
+ * rounding of the accumulator); has_clamp clamps to [clamp_lo, clamp_hi].
+ * Replaces GEMM.get_callable() -> (A, B, C) of iron/operators/gemm/op.py:21-231
+ * (b_col_maj=True; other layouts via iron_transpose_bf16 / operand swap) and
+ * flm.GEMM of iron/operators/flm/gemm/op.py:64-499 (epilogue + clamp, B packed
+ * to (N,K) by pack_B). */
+int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K, long long ldc, int epilogue,
+                      int has_clamp, float clamp_lo, float clamp_hi, void* stream);
+
+/* out (cols, rows) = in (rows, cols)^T, bf16. Layout glue for GEMM's
+ * row-major B (the role of iron/operators/transpose/op.py:18-120). */
+int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream);
+
+/* --------------------------------------------------------- Llama glue ---- */
+
+/* out[i] = table[ids[i]] (rows of dim bf16; zeros for ids outside [0,vocab)).
+ * ids is a device int32 array, so a captured decode graph reads the token it
+ * produced. Replaces the host-side embedding of
+ * iron/applications/llama_3.2_1b/llama_npu.py:1171-1184. */
+int iron_embedding(const void* table, const int* ids, void* out, int n, int dim, int vocab, void* stream);
+
+/* Greedy argmax over n bf16 logits (first index on ties) -> token_out[0].
+ * When pos (device int32) is given: history[*pos] = token if *pos <
+ * history_cap (history may be NULL), then *pos += 1. Keeps the greedy decode
+ * loop on the GPU (the harness samples on the CPU:
+ * iron/applications/llama_3.2_1b/llama_inference_harness.py:146-169). */
+int iron_argmax_bf16(const void* x, int n, int* token_out, int* pos, int* history, int history_cap, void* stream);
+
+/* Prefill scatter: qkv (seq, (H+2Hkv)*64) -> q_out (seq, H*64) rotated,
+ * k_cache[:, pos0+s] rotated, v_cache[:, pos0+s] = v (two-halves RoPE with
+ * row pos0+s of the fp32 [cos,sin] table; bf16 rounding). Replaces the
+ * prefill RoPE + KV copy steps of llama_npu.py:881-947. */
+int iron_qkv_rope_scatter(const void* qkv, const float* angles, int angle_rows, void* q_out, void* k_cache,
+                          void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim, int max_len, int pos0,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,12 @@ SIGNATURES: dict[str, list] = {
     "iron_rope": [_P, _P, _I, _P, _I, _I, _I, _I, _P],
     "iron_gqa_decode": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P],
     "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
+    "iron_gemm_bf16_nt": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _P],
+    "iron_transpose_bf16": [_P, _P, _I, _I, _P],
+    "iron_quantize_i4g32": [_P, _P, _P, _I, _I, _P],
+    "iron_embedding": [_P, _P, _P, _I, _I, _I, _P],
+    "iron_argmax_bf16": [_P, _I, _P, _P, _P, _I, _P],
+    "iron_qkv_rope_scatter": [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
 }
 
 # ... except these queries, which return a value.

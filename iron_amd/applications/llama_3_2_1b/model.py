@@ -1,0 +1,402 @@
+"""Llama-3.2-1B on MI355X: the reference application's forward pass
+(iron/applications/llama_3.2_1b/llama_npu.py) rebuilt on the HIP kernels.
+
+Decode (one token) is 5 kernels per layer plus 3, all reading the token id and
+position from device memory:
+
+    embedding(token)                                     iron_embedding
+    per layer:
+      qkv = Wqkv . rmsnorm(x)                            iron_gemv_i4g32_fused (norm fused)
+      attn = gqa(rope(q), rope(k) -> cache, v -> cache)  iron_gqa_decode (split-K, pos on device)
+      x  += Wo . attn                                    iron_gemv_i4g32_fused (residual fused)
+      h   = silu(Wg . rmsnorm(x)) * (Wu . rmsnorm(x))    iron_gemv_i4g32_fused (pair + norm)
+      x  += Wd . h                                       iron_gemv_i4g32_fused (residual fused)
+    logits = Wemb . rmsnorm(x)                           iron_gemv_bf16_fused (tied head)
+    token, pos += 1                                      iron_argmax_bf16
+
+so the step is captured once as a HIP graph and replayed for every token with
+no host synchronisation (the reference's single fused decode dispatch,
+llama_npu.py:459-584, is the analogue). Prefill runs the same layers on bf16
+MFMA GEMMs over the prompt (iron_gemm_bf16_nt) with causal flash attention
+(iron_attention_prefill), replacing the reference's GEMM + CPU-softmax path
+(llama_npu.py:1028-1149).
+
+Weights: every linear layer is quantised once to int4 group-32
+(iron_quantize_i4g32). Decode streams the int4 codes; prefill uses bf16
+copies produced by dequantising those same codes (iron_dequant_i4), so both
+phases compute with identical effective weights. The tied embedding / LM
+head stays bf16 (optionally int4 with ``head_int4``).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from ... import _lib
+
+BF16 = torch.bfloat16
+
+
+@dataclass
+class LlamaConfig:
+    """Model constants of llama_inference_harness.py:31-41 plus the KV capacity."""
+
+    vocab_size: int = 128256
+    emb_dim: int = 2048
+    n_layers: int = 16
+    n_heads: int = 32
+    n_kv_groups: int = 8
+    hidden_dim: int = 8192
+    rope_base: float = 500000.0
+    rope_scaling: dict | None = field(
+        default_factory=lambda: {"factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                 "original_context_length": 8192}
+    )
+    eps: float = 1e-5
+    max_seq_len: int = 4608
+    int4: bool = True
+    head_int4: bool = False
+
+    @property
+    def head_dim(self) -> int:
+        return self.emb_dim // self.n_heads
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_groups) * self.head_dim
+
+    def validate(self) -> None:
+        if self.head_dim != 64:
+            raise ValueError(f"head_dim must be 64 (emb_dim / n_heads = {self.head_dim})")
+        if self.n_heads % self.n_kv_groups or self.n_heads // self.n_kv_groups not in (1, 2, 4, 8):
+            raise ValueError("n_heads / n_kv_groups must be 1, 2, 4 or 8")
+        if self.emb_dim % 64 or self.hidden_dim % 64:
+            raise ValueError("emb_dim and hidden_dim must be multiples of 64")
+
+
+def compute_rope_angles(head_dim: int, context_length: int, base: float, scaling: dict | None) -> torch.Tensor:
+    """fp32 table (context_length, head_dim) of interleaved [cos, sin] pairs.
+
+    The layout of llama_inference_harness.py:109-123; inverse frequencies with
+    the llama3 band scaling of iron/operators/rope/reference.py:26-52 when
+    ``scaling`` is given (BASELINE: factor 32, low 1, high 4, original 8192).
+    """
+    inv = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    if scaling is not None:
+        lo_wl = scaling["original_context_length"] / scaling["low_freq_factor"]
+        hi_wl = scaling["original_context_length"] / scaling["high_freq_factor"]
+        wl = 2 * math.pi / inv
+        scaled = torch.where(wl > lo_wl, inv / scaling["factor"], inv)
+        smooth = (scaling["original_context_length"] / wl - scaling["low_freq_factor"]) / (
+            scaling["high_freq_factor"] - scaling["low_freq_factor"]
+        )
+        blended = (1 - smooth) * inv / scaling["factor"] + smooth * inv
+        inv = torch.where((wl <= lo_wl) & (wl >= hi_wl), blended, scaled)
+    ang = torch.outer(torch.arange(context_length, dtype=torch.float32), inv)
+    table = torch.empty(context_length, head_dim, dtype=torch.float32)
+    table[:, 0::2] = torch.cos(ang)
+    table[:, 1::2] = torch.sin(ang)
+    return table
+
+
+def random_weights(cfg: LlamaConfig, device, seed: int = 0, std: float = 0.02) -> dict:
+    """Random-init Llama-shaped weights (Hugging Face names, bf16, on ``device``):
+    linear and embedding weights ~N(0, std^2), norm weights ~N(1, 0.1^2)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def normal(*shape, mean=0.0, s=std):
+        return (torch.randn(*shape, generator=g, device=device) * s + mean).to(BF16)
+
+    E, H, Hd = cfg.emb_dim, cfg.hidden_dim, cfg.head_dim
+    w = {"model.embed_tokens.weight": normal(cfg.vocab_size, E), "model.norm.weight": normal(E, mean=1.0, s=0.1)}
+    for i in range(cfg.n_layers):
+        p = f"model.layers.{i}."
+        w[p + "input_layernorm.weight"] = normal(E, mean=1.0, s=0.1)
+        w[p + "post_attention_layernorm.weight"] = normal(E, mean=1.0, s=0.1)
+        w[p + "self_attn.q_proj.weight"] = normal(cfg.n_heads * Hd, E)
+        w[p + "self_attn.k_proj.weight"] = normal(cfg.n_kv_groups * Hd, E)
+        w[p + "self_attn.v_proj.weight"] = normal(cfg.n_kv_groups * Hd, E)
+        w[p + "self_attn.o_proj.weight"] = normal(E, cfg.n_heads * Hd)
+        w[p + "mlp.gate_proj.weight"] = normal(H, E)
+        w[p + "mlp.up_proj.weight"] = normal(H, E)
+        w[p + "mlp.down_proj.weight"] = normal(E, H)
+    return w
+
+
+class Linear:
+    """One linear layer (out_features, in_features) held as int4-g32 codes +
+    scales for decode and the matching dequantised bf16 matrix for prefill."""
+
+    def __init__(self, weight: torch.Tensor, int4: bool, stream: int):
+        self.N, self.K = weight.shape
+        dev = weight.device
+        if int4:
+            if self.K % 32:
+                raise ValueError(f"in_features {self.K} must be a multiple of 32 for int4")
+            self.codes = torch.empty(self.N, self.K // 2, dtype=torch.uint8, device=dev)
+            self.scales = torch.empty(self.N, self.K // 32, dtype=BF16, device=dev)
+            self.bf16 = torch.empty(self.N, self.K, dtype=BF16, device=dev)
+            w = weight.contiguous()
+            _lib.call("iron_quantize_i4g32", w.data_ptr(), self.codes.data_ptr(), self.scales.data_ptr(), self.N,
+                      self.K, stream)
+            _lib.call("iron_dequant_i4", self.codes.data_ptr(), self.scales.data_ptr(), self.bf16.data_ptr(), self.N,
+                      self.K, 32, 1, stream)
+        else:
+            self.codes = self.scales = None
+            self.bf16 = weight.contiguous()
+        self.int4 = int4
+
+    def gemv(self, x, y, stream, norm_w=None, eps=0.0, residual=None, pair: "Linear | None" = None):
+        """y = [silu](W . norm(x)) [* (W2 . norm(x))] [+ residual] on one token."""
+        if self.int4:
+            _lib.call("iron_gemv_i4g32_fused", self.codes.data_ptr(), self.scales.data_ptr(),
+                      _lib.ptr(pair.codes if pair else None), _lib.ptr(pair.scales if pair else None), x.data_ptr(),
+                      y.data_ptr(), self.N, self.K, 1, _lib.ptr(norm_w), float(eps), _lib.ptr(residual), 0, stream)
+        else:
+            _lib.call("iron_gemv_bf16_fused", self.bf16.data_ptr(), _lib.ptr(pair.bf16 if pair else None),
+                      x.data_ptr(), y.data_ptr(), self.N, self.K, _lib.ptr(norm_w), float(eps), _lib.ptr(residual),
+                      0, stream)
+
+    def gemm(self, X, Y, rows, stream):
+        """Y (rows, N) = X (rows, K) . W^T on bf16 MFMA."""
+        _lib.call("iron_gemm_bf16_nt", X.data_ptr(), self.bf16.data_ptr(), Y.data_ptr(), rows, self.N, self.K,
+                  self.N, 0, 0, 0.0, 0.0, stream)
+
+
+class LlamaHIP:
+    """Llama-3.2-1B-shaped model on one GPU: weights, KV caches and the decode graph."""
+
+    def __init__(self, cfg: LlamaConfig, weights: dict, device=None):
+        cfg.validate()
+        self.cfg = cfg
+        self.device = torch.device(device) if device is not None else torch.device("cuda", 0)
+        _lib.load()
+        s = self._stream()
+        E, Hd = cfg.emb_dim, cfg.head_dim
+        dev = self.device
+        w = {k: v.to(dev, BF16).contiguous() for k, v in weights.items()}
+        self.embed = w["model.embed_tokens.weight"]
+        self.final_norm = w["model.norm.weight"]
+        self.head = Linear(self.embed, cfg.head_int4, s) if cfg.head_int4 else None
+        self.layers = []
+        for i in range(cfg.n_layers):
+            p = f"model.layers.{i}."
+            qkv = torch.cat([w[p + "self_attn.q_proj.weight"], w[p + "self_attn.k_proj.weight"],
+                             w[p + "self_attn.v_proj.weight"]], dim=0)
+            self.layers.append({
+                "attn_norm": w[p + "input_layernorm.weight"],
+                "ffn_norm": w[p + "post_attention_layernorm.weight"],
+                "qkv": Linear(qkv, cfg.int4, s),
+                "o": Linear(w[p + "self_attn.o_proj.weight"], cfg.int4, s),
+                "gate": Linear(w[p + "mlp.gate_proj.weight"], cfg.int4, s),
+                "up": Linear(w[p + "mlp.up_proj.weight"], cfg.int4, s),
+                "down": Linear(w[p + "mlp.down_proj.weight"], cfg.int4, s),
+            })
+        del w
+        L = cfg.max_seq_len
+        self.k_cache = [torch.zeros(cfg.n_kv_groups, L, Hd, dtype=BF16, device=dev) for _ in range(cfg.n_layers)]
+        self.v_cache = [torch.zeros(cfg.n_kv_groups, L, Hd, dtype=BF16, device=dev) for _ in range(cfg.n_layers)]
+        self.angles = compute_rope_angles(Hd, L, cfg.rope_base, cfg.rope_scaling).to(dev)
+        ws = _lib.query("iron_gqa_decode_workspace_bytes", cfg.n_heads, cfg.n_kv_groups, Hd, L)
+        self.attn_ws = torch.zeros(int(ws), dtype=torch.uint8, device=dev)
+        # decode buffers (fixed addresses: the captured graph refers to them)
+        self.x = torch.zeros(E, dtype=BF16, device=dev)
+        self.qkv = torch.zeros(cfg.qkv_dim, dtype=BF16, device=dev)
+        self.attn = torch.zeros(cfg.n_heads * Hd, dtype=BF16, device=dev)
+        self.h = torch.zeros(cfg.hidden_dim, dtype=BF16, device=dev)
+        self.logits = torch.zeros(cfg.vocab_size, dtype=BF16, device=dev)
+        self.xn = torch.zeros(E, dtype=BF16, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.history = torch.zeros(L, dtype=torch.int32, device=dev)
+        self.host_pos = 0
+        self.graph = None
+        self._prefill_bufs = {}
+        torch.cuda.synchronize(dev)
+
+    # ------------------------------------------------------------ helpers
+    def _stream(self) -> int:
+        return _lib.stream_handle(self.device)
+
+    def effective_weights(self) -> dict:
+        """The weights the model computes with (dequantised int4 as bf16), HF names."""
+        cfg = self.cfg
+        q_rows, kv_rows = cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
+        out = {"model.embed_tokens.weight": self.embed, "model.norm.weight": self.final_norm}
+        for i, L in enumerate(self.layers):
+            p = f"model.layers.{i}."
+            qkv = L["qkv"].bf16
+            out[p + "self_attn.q_proj.weight"] = qkv[:q_rows]
+            out[p + "self_attn.k_proj.weight"] = qkv[q_rows : q_rows + kv_rows]
+            out[p + "self_attn.v_proj.weight"] = qkv[q_rows + kv_rows :]
+            out[p + "self_attn.o_proj.weight"] = L["o"].bf16
+            out[p + "mlp.gate_proj.weight"] = L["gate"].bf16
+            out[p + "mlp.up_proj.weight"] = L["up"].bf16
+            out[p + "mlp.down_proj.weight"] = L["down"].bf16
+            out[p + "input_layernorm.weight"] = L["attn_norm"]
+            out[p + "post_attention_layernorm.weight"] = L["ffn_norm"]
+        return out
+
+    def reset(self) -> None:
+        """Empty the KV cache (positions restart at 0); cache contents need no clearing."""
+        self.host_pos = 0
+        self.pos.copy_(torch.zeros(1, dtype=torch.int32))
+
+    # ------------------------------------------------------------ decode
+    def decode_step(self) -> None:
+        """Enqueue one decode step: token/pos from device memory, next token and pos+1 back."""
+        cfg, s = self.cfg, self._stream()
+        Hd, q_rows, kv_rows = cfg.head_dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
+        _lib.call("iron_embedding", self.embed.data_ptr(), self.token.data_ptr(), self.x.data_ptr(), 1, cfg.emb_dim,
+                  cfg.vocab_size, s)
+        q = self.qkv[:q_rows]
+        k = self.qkv[q_rows : q_rows + kv_rows]
+        v = self.qkv[q_rows + kv_rows :]
+        scale = 1.0 / math.sqrt(Hd)
+        for i, L in enumerate(self.layers):
+            L["qkv"].gemv(self.x, self.qkv, s, norm_w=L["attn_norm"], eps=cfg.eps)
+            _lib.call("iron_gqa_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
+                      self.v_cache[i].data_ptr(), self.angles.data_ptr(), self.angles.shape[0], self.attn.data_ptr(),
+                      self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, 0,
+                      self.pos.data_ptr(), scale, s)
+            L["o"].gemv(self.attn, self.x, s, residual=self.x)
+            L["gate"].gemv(self.x, self.h, s, norm_w=L["ffn_norm"], eps=cfg.eps, pair=L["up"])
+            L["down"].gemv(self.h, self.x, s, residual=self.x)
+        if self.head is not None:
+            self.head.gemv(self.x, self.logits, s, norm_w=self.final_norm, eps=cfg.eps)
+        else:
+            _lib.call("iron_gemv_bf16_fused", self.embed.data_ptr(), None, self.x.data_ptr(), self.logits.data_ptr(),
+                      cfg.vocab_size, cfg.emb_dim, self.final_norm.data_ptr(), float(cfg.eps), None, 0, s)
+        _lib.call("iron_argmax_bf16", self.logits.data_ptr(), cfg.vocab_size, self.token.data_ptr(),
+                  self.pos.data_ptr(), self.history.data_ptr(), cfg.max_seq_len, s)
+
+    def _warmup(self) -> None:
+        """Run every decode kernel once eagerly (code objects load before capture).
+
+        Uses the last cache slot, which a later step at that position rewrites
+        before any attention reads it; token and position are restored.
+        """
+        tok = self.token.clone()
+        pos = self.pos.clone()
+        self.pos.fill_(self.cfg.max_seq_len - 1)
+        self.decode_step()
+        self.token.copy_(tok)
+        self.pos.copy_(pos)
+        torch.cuda.synchronize(self.device)
+
+    def capture_decode_graph(self) -> None:
+        """Capture decode_step() once as a HIP graph (replayed per token)."""
+        self._warmup()
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                self.decode_step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = g
+
+    def decode(self, n_steps: int, use_graph: bool = True) -> None:
+        """Run n_steps greedy decode steps from the current token and position."""
+        if self.host_pos + n_steps > self.cfg.max_seq_len:
+            raise ValueError(f"decoding {n_steps} steps from position {self.host_pos} exceeds the KV capacity "
+                             f"{self.cfg.max_seq_len}")
+        if use_graph and self.graph is None:
+            self.capture_decode_graph()
+        for _ in range(n_steps):
+            if use_graph:
+                self.graph.replay()
+            else:
+                self.decode_step()
+        self.host_pos += n_steps
+
+    # ------------------------------------------------------------ prefill
+    def _pbufs(self, S: int):
+        b = self._prefill_bufs.get(S)
+        if b is None:
+            cfg, dev = self.cfg, self.device
+            E, Hd = cfg.emb_dim, cfg.head_dim
+            b = {
+                "ids": torch.zeros(S, dtype=torch.int32, device=dev),
+                "X": torch.zeros(S, E, dtype=BF16, device=dev),
+                "Xn": torch.zeros(S, E, dtype=BF16, device=dev),
+                "QKV": torch.zeros(S, cfg.qkv_dim, dtype=BF16, device=dev),
+                "Q": torch.zeros(S, cfg.n_heads * Hd, dtype=BF16, device=dev),
+                "O": torch.zeros(S, cfg.n_heads * Hd, dtype=BF16, device=dev),
+                "T": torch.zeros(S, E, dtype=BF16, device=dev),
+                "G": torch.zeros(S, cfg.hidden_dim, dtype=BF16, device=dev),
+                "U": torch.zeros(S, cfg.hidden_dim, dtype=BF16, device=dev),
+            }
+            self._prefill_bufs[S] = b
+        return b
+
+    def prefill(self, token_ids) -> None:
+        """Process the prompt at positions pos..pos+S-1; leaves logits of the last
+        position in self.logits and the greedy next token in self.token."""
+        cfg, s = self.cfg, self._stream()
+        ids = torch.as_tensor(token_ids, dtype=torch.int32).reshape(-1)
+        S = int(ids.numel())
+        pos0 = self.host_pos
+        if S == 0 or pos0 + S > cfg.max_seq_len:
+            raise ValueError(f"prompt of {S} tokens at position {pos0} does not fit the KV capacity {cfg.max_seq_len}")
+        b = self._pbufs(S)
+        b["ids"].copy_(ids)
+        E, Hd = cfg.emb_dim, cfg.head_dim
+        X, Xn, T = b["X"], b["Xn"], b["T"]
+        _lib.call("iron_embedding", self.embed.data_ptr(), b["ids"].data_ptr(), X.data_ptr(), S, E, cfg.vocab_size, s)
+        scale = 1.0 / math.sqrt(Hd)
+        first = True
+        for i, L in enumerate(self.layers):
+            if first:
+                _lib.call("iron_rmsnorm", X.data_ptr(), None, L["attn_norm"].data_ptr(), Xn.data_ptr(), None, S, E,
+                          float(cfg.eps), s)
+                first = False
+            else:  # X += T (previous FFN output), Xn = norm(X)
+                _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), L["attn_norm"].data_ptr(), Xn.data_ptr(),
+                          X.data_ptr(), S, E, float(cfg.eps), s)
+            L["qkv"].gemm(Xn, b["QKV"], S, s)
+            _lib.call("iron_qkv_rope_scatter", b["QKV"].data_ptr(), self.angles.data_ptr(), self.angles.shape[0],
+                      b["Q"].data_ptr(), self.k_cache[i].data_ptr(), self.v_cache[i].data_ptr(), S, cfg.n_heads,
+                      cfg.n_kv_groups, Hd, cfg.max_seq_len, pos0, s)
+            _lib.call("iron_attention_prefill", b["Q"].data_ptr(), self.k_cache[i].data_ptr(),
+                      self.v_cache[i].data_ptr(), b["O"].data_ptr(), cfg.n_heads, cfg.n_kv_groups, S, pos0 + S, Hd,
+                      Hd, cfg.n_heads * Hd, cfg.max_seq_len * Hd, Hd, Hd, cfg.n_heads * Hd, S, 1, pos0, scale, s)
+            L["o"].gemm(b["O"], T, S, s)
+            _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), L["ffn_norm"].data_ptr(), Xn.data_ptr(),
+                      X.data_ptr(), S, E, float(cfg.eps), s)
+            L["gate"].gemm(Xn, b["G"], S, s)
+            L["up"].gemm(Xn, b["U"], S, s)
+            _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(), S * cfg.hidden_dim, s)
+            L["down"].gemm(b["G"], T, S, s)
+        _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), self.final_norm.data_ptr(), Xn.data_ptr(),
+                  X.data_ptr(), S, E, float(cfg.eps), s)
+        last = Xn[S - 1]
+        if self.head is not None:
+            self.head.gemv(last, self.logits, s)
+        else:
+            _lib.call("iron_gemv_bf16", self.embed.data_ptr(), last.data_ptr(), self.logits.data_ptr(),
+                      cfg.vocab_size, E, 1, 0, s)
+        self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
+        _lib.call("iron_argmax_bf16", self.logits.data_ptr(), cfg.vocab_size, self.token.data_ptr(),
+                  self.pos.data_ptr(), self.history.data_ptr(), cfg.max_seq_len, s)
+        self.host_pos = pos0 + S
+
+    def set_token(self, token: int) -> None:
+        """Override the next input token (teacher forcing)."""
+        self.token.copy_(torch.tensor([int(token)], dtype=torch.int32))
+
+    def generate(self, prompt_ids, n_tokens: int, use_graph: bool = True) -> list[int]:
+        """Greedy generation: prefill the prompt, then n_tokens-1 decode steps.
+        Returns the n_tokens generated ids (read back once at the end)."""
+        self.reset()
+        self.prefill(prompt_ids)
+        S = self.host_pos
+        if n_tokens > 1:
+            self.decode(n_tokens - 1, use_graph=use_graph)
+        torch.cuda.synchronize(self.device)
+        return self.history[S - 1 : S - 1 + n_tokens].tolist()

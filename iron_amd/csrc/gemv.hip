@@ -564,3 +564,57 @@ extern "C" int iron_dequant_i4_payload(const void* payload, void* out, long long
                      static_cast<uint16_t*>(out), size, tile_size, group_size, is_signed);
   return check_launch("dequant_i4_payload");
 }
+
+// ---------------------------------------------------------------------------
+// Symmetric int4 group-32 quantiser (weight preparation, not on the hot
+// path): per group of 32, scale = bf16(max|w| / 7), q = clamp(rint(w / scale),
+// -8, 7), packed two per byte along K, low nibble first.
+// ---------------------------------------------------------------------------
+namespace iron {
+namespace {
+__global__ __launch_bounds__(256) void quantize_i4g32_kernel(const uint16_t* __restrict__ W, uint8_t* __restrict__ codes,
+                                                             uint16_t* __restrict__ scales, long long groups) {
+  const long long g = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (g >= groups) return;
+  const uint4* src = reinterpret_cast<const uint4*>(W + g * 32);
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint4 c = src[q];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[q * 8 + 2 * e] = lo_bf16(w[e]);
+      v[q * 8 + 2 * e + 1] = hi_bf16(w[e]);
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, 1e-8f);
+  const uint16_t sb = f32_to_bf16(amax / 7.0f);
+  const float s = bf16_to_f32(sb);
+  uint32_t packed[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    float q = rintf(v[i] / s);
+    q = fminf(fmaxf(q, -8.f), 7.f);
+    const uint32_t nib = static_cast<uint32_t>(static_cast<int>(q)) & 0xfu;
+    packed[i >> 3] |= nib << (4 * (i & 7));
+  }
+  reinterpret_cast<uint4*>(codes + g * 16)[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  scales[g] = sb;
+}
+}  // namespace
+}  // namespace iron
+
+extern "C" int iron_quantize_i4g32(const void* W, void* codes, void* scales, int N, int K, void* stream) {
+  IRON_REQUIRE(W && codes && scales, "iron_quantize_i4g32: null pointer");
+  IRON_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "iron_quantize_i4g32: N=%d K=%d (K must be a multiple of 32)", N, K);
+  IRON_REQUIRE(aligned16(W) && aligned16(codes), "iron_quantize_i4g32: W and codes must be 16-byte aligned");
+  const long long groups = static_cast<long long>(N) * (K / 32);
+  hipLaunchKernelGGL(quantize_i4g32_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(W), static_cast<uint8_t*>(codes),
+                     static_cast<uint16_t*>(scales), groups);
+  return check_launch("quantize_i4g32");
+}

@@ -11,6 +11,7 @@ _OPERATOR_MODULES = {
     "Dequant": "dequant",
     "ElementwiseAdd": "elementwise_add",
     "ElementwiseMul": "elementwise_mul",
+    "GEMM": "gemm",
     "GEMV": "gemv",
     "GEMVInt4": "gemv_int4",
     "GQADecode": "gqa_decode",
@@ -21,7 +22,7 @@ _OPERATOR_MODULES = {
     "Softmax": "softmax",
 }
 
-_SUBPACKAGES: tuple = ()
+_SUBPACKAGES: tuple = ("flm",)
 
 __all__ = sorted(set(_OPERATOR_MODULES) | set(_SUBPACKAGES))
 

@@ -1,0 +1,99 @@
+"""GPU parity: GEMM and flm.GEMM (bf16 MFMA) against the CPU oracle.
+
+Shapes and layouts follow the reference tests: iron/operators/gemm/test.py
+(regular list; rel/abs 0.005) and iron/operators/flm/gemm/test.py:54-113 (NPU2
+list; abs bound 0.004 * K * mean|a| * mean|b|, rel 0.04; activation inputs
+scaled by 0.5), plus the Llama prefill shapes of BASELINE config 5.
+"""
+
+import pytest
+import torch
+
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+
+
+@pytest.mark.parametrize(
+    "M,K,N,b_col_maj,c_col_maj",
+    [
+        (2048, 2048, 2048, False, False),
+        (2048, 2048, 2048, True, False),
+        (2048, 2048, 2048, True, True),
+        (384, 1536, 1792, True, False),
+        (1792, 896, 1152, False, True),
+        (896, 1792, 640, False, True),
+        (192, 384, 64, False, False),
+        (192, 384, 64, True, True),
+        (64, 512, 256, True, False),
+        (2048, 64, 8192, False, False),
+        (100, 192, 130, True, False),
+    ],
+)
+def test_gemm(gpu, M, K, N, b_col_maj, c_col_maj):
+    from iron_amd.operators import GEMM
+
+    g = ops.gemm_golden(M, K, N, b_col_maj=b_col_maj)
+    ref = g["output"].T.contiguous() if c_col_maj else g["output"]
+    op = GEMM(M=M, K=K, N=N, b_col_maj=b_col_maj, c_col_maj=c_col_maj)
+    C = torch.empty(ref.shape, dtype=BF16, device=gpu)
+    op.get_callable()(g["input"].to(gpu), g["input_b"].to(gpu), C)
+    torch.cuda.synchronize()
+    errs = ops.verify_buffer(C, ref, rel_tol=0.005, abs_tol=0.005)
+    assert not errs, f"{len(errs)} mismatches of {ref.numel()}"
+
+
+FLM = [
+    (256, 512, 1024, "none", None),
+    (512, 1024, 2048, "none", None),
+    (256, 512, 1536, "none", None),
+    (256, 512, 128, "none", None),
+    (256, 512, 1024, "silu", None),
+    (256, 512, 1024, "gelu", None),
+    (256, 512, 1024, "none", (-2.0, 2.0)),
+    (1024, 2048, 2048, "none", None),
+    (1024, 2560, 2560, "none", None),
+    (512, 1536, 1536, "silu", None),
+    (256, 512, 1024, "sigmoid", None),
+    (512, 1024, 2048, "silu", (-4.0, 4.0)),
+    (1024, 1536, 6144, "none", None),
+    (1024, 2560, 10240, "none", None),
+]
+
+
+@pytest.mark.parametrize("M,K,N,epilogue,clamp", FLM)
+def test_flm_gemm(gpu, M, K, N, epilogue, clamp):
+    from iron_amd.operators import flm
+
+    scale = 4.0 if epilogue == "none" else 0.5
+    g = ops.flm_gemm_golden(M, K, N, epilogue=epilogue, clamp=clamp, scale=scale)
+    op = flm.GEMM(M=M, K=K, N=N, epilogue=epilogue, clamp=clamp)
+    C = torch.empty(M, N, dtype=BF16, device=gpu)
+    op.get_callable()(g["input"].to(gpu), op.pack_B(g["input_b"]).to(gpu), C)
+    torch.cuda.synchronize()
+    mass = K * g["input"].abs().float().mean() * g["input_b"].abs().float().mean()
+    errs = ops.verify_buffer(C, g["output"], rel_tol=0.04, abs_tol=float(0.004 * mass))
+    assert not errs, f"{len(errs)} mismatches"
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 2048), (512, 2048, 512), (512, 2048, 8192), (512, 8192, 2048),
+                                   (13, 2048, 3072)])
+def test_prefill_gemm_shapes(gpu, M, K, N):
+    """Config 5 prefill projections (A activations, B = nn.Linear weight (N, K)), fp32-accumulated
+    reference; BASELINE bar max-abs 2e-2 / rel-L2 1e-2 on N(0,1) activations x N(0,0.02^2) weights."""
+    from iron_amd import _lib
+
+    gen = torch.Generator().manual_seed(M + K + N)
+    A = torch.randn(M, K, generator=gen).to(BF16)
+    W = (torch.randn(N, K, generator=gen) * 0.02).to(BF16)
+    ref = A.float() @ W.float().T
+    Ad, Wd = A.to(gpu), W.to(gpu)
+    C = torch.empty(M, N, dtype=BF16, device=gpu)
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+              _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    max_abs, rel_l2 = ops.max_abs_rel_l2(C, ref)
+    assert rel_l2 <= 1e-2
+    bad = ops.within_bf16_ulps(C, ref, n_ulp=1.0, atol=1e-5 * float(ref.abs().max()))
+    assert not bad, bad[:5]
