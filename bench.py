@@ -1,25 +1,30 @@
 #!/usr/bin/env python3
-"""Benchmark of the IRON decode operator path on one MI355X.
+"""Benchmark of the IRON decode/prefill operator path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-model]
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
-batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes.
-A step is one launch over one weight copy; the copies rotate through a pool
-of >= 512 MiB so the 256 MiB Infinity Cache cannot hold the working set and
-every step streams its weights from HBM. Inputs are resident in HBM before
-the timed region.
+batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
+(9,457,664 B per step). A step is one launch over one weight copy; copies
+rotate through a pool of >= 512 MiB so the 256 MiB Infinity Cache cannot hold
+the working set. Inputs are resident in HBM before the timed region; the
+timed region is exactly K launches on one stream between two synchronizes.
 
-``roofline`` is measured on the kernel's own stream with HIP events, one
-start/stop pair per launch, averaged; ``cpu_baseline`` times the CPU oracle
-(torch, dequantize then matvec) on the host cores on a bounded sample.
-Extra figures for the other BASELINE configurations go under ``extra``.
+``roofline``: algorithmic bytes / the kernel's mean device execution time,
+measured with HIP events that the launch itself records at the kernel's start
+and end (iron_time_next_launch -> hipExtLaunchKernel) on the launch stream.
+``cpu_baseline``: the CPU oracle (torch: dequantise, then fp32 matvec) timed
+on the host cores on a bounded sample. ``extra`` carries the other BASELINE
+configurations: bf16 GEMV (cfg 1), GQA decode (cfg 3), SwiGLU block bf16 and
+int4 (cfg 4), the prefill GEMM and the Llama-3.2-1B-shaped model (cfg 5:
+prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096 window).
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -35,108 +40,316 @@ POOL_BYTES = 640 << 20  # rotate through > 512 MiB of distinct weights
 METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 
 
-def _events(torch, n):
-    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+class HipEvents:
+    """hipEvent_t pairs from the HIP runtime torch loaded (libamdhip64.so.7).
 
-
-def time_steps(torch, launch, steps, warmup):
-    """Warm up, then time exactly ``steps`` launches bracketed by synchronize.
-
-    Returns (wall_ms_total, mean_kernel_us) where the kernel time comes from a
-    start/stop event pair around each launch on the launch stream.
+    Events armed with iron_time_next_launch are recorded by the launch itself,
+    which torch.cuda.Event does not track, so they are created and read here.
     """
-    for i in range(warmup):
-        launch(i)
-    torch.cuda.synchronize()
-    starts, stops = _events(torch, steps), _events(torch, steps)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record()
-        launch(warmup + i)
-        stops[i].record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    per = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, stops))
-    # mean of the central 80% (drops the first-touch and preemption outliers)
-    lo, hi = len(per) // 10, len(per) - len(per) // 10
-    core = per[lo:hi] or per
-    return wall_ms, sum(core) / len(core)
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        e = self.ct.c_void_p()
+        if self.hip.hipEventCreate(self.ct.byref(e)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return e.value
+
+    def elapsed_ms(self, a, b):
+        if self.hip.hipEventSynchronize(b) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        ms = self.ct.c_float()
+        rc = self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def destroy(self, e):
+        self.hip.hipEventDestroy(e)
 
 
-def time_back_to_back(torch, launch, n):
-    """Events around ``n`` back-to-back launches: per-launch time incl. gaps (us)."""
-    e0, e1 = _events(torch, 2)
-    torch.cuda.synchronize()
-    e0.record()
-    for i in range(n):
-        launch(i)
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / n
+class Timer:
+    """Kernel device time (armed events) and stream wall time for launch closures."""
+
+    def __init__(self, torch, lib):
+        self.torch, self.lib = torch, lib
+        self.ev = HipEvents()
+
+    def kernel_us(self, launch, n, offset=0):
+        """Mean device time of the first kernel of launch(i), over n launches (microseconds)."""
+        torch = self.torch
+        ev = [(self.ev.create(), self.ev.create()) for _ in range(n)]
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(ev):
+            rc = self.lib.iron_time_next_launch(a, b)
+            assert rc == 0
+            launch(offset + i)
+        torch.cuda.synchronize()
+        t = sorted(self.ev.elapsed_ms(a, b) * 1e3 for a, b in ev)
+        for a, b in ev:
+            self.ev.destroy(a)
+            self.ev.destroy(b)
+        core = t[len(t) // 10 : len(t) - len(t) // 10] or t
+        return sum(core) / len(core)
+
+    def wall_ms(self, launch, n, offset=0):
+        """Events around n back-to-back launches on the current stream (milliseconds)."""
+        torch = self.torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for i in range(n):
+            launch(offset + i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b)
 
 
-def bench_gemv_int4(torch, dev, steps, warmup):
+def _check(lib, rc):
+    if rc:
+        raise RuntimeError(lib.iron_last_error().decode())
+
+
+def bench_gemv_int4(torch, lib, tm, dev, steps, warmup):
     from iron_amd import _lib
     from oracle import configs
 
     M, K = 8192, 2048
     codes, scales, x = configs.cfg2_gemv_int4(M=M, K=K)
-    nbytes = M * K // 2 + 2 * M * K // 32 + 2 * K + 2 * M  # 9,457,664 B algorithmic
+    nbytes = M * K // 2 + 2 * M * K // 32 + 2 * K + 2 * M
     copies = max(2, POOL_BYTES // (codes.numel() + 2 * scales.numel()))
     C = [codes.to(dev) for _ in range(copies)]
     S = [scales.to(dev) for _ in range(copies)]
     xd = x.to(dev)
     y = torch.empty(M, dtype=torch.bfloat16, device=dev)
     stream = _lib.stream_handle(dev)
-    lib = _lib.load()
-    fn = lib.iron_gemv_i4g32
 
     def launch(i):
-        rc = fn(C[i % copies].data_ptr(), S[i % copies].data_ptr(), xd.data_ptr(), y.data_ptr(), M, K, 1, stream)
-        if rc:
-            raise RuntimeError(lib.iron_last_error().decode())
+        _check(lib, lib.iron_gemv_i4g32(C[i % copies].data_ptr(), S[i % copies].data_ptr(), xd.data_ptr(),
+                                        y.data_ptr(), M, K, 1, stream))
 
-    wall_ms, kern_us = time_steps(torch, launch, steps, warmup)
-    b2b_us = time_back_to_back(torch, launch, 200)
-    return {
-        "bytes": nbytes,
-        "wall_ms": wall_ms,
-        "kernel_us": kern_us,
-        "b2b_us": b2b_us,
-        "pool_copies": copies,
-        "inputs": (codes, scales, x),
-    }
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    wall = tm.wall_ms(launch, steps, offset=warmup)
+    host_s = time.perf_counter() - t0
+    kern = tm.kernel_us(launch, min(steps, 1000), offset=warmup + steps)
+    return {"bytes": nbytes, "wall_ms": wall, "host_s": host_s, "kernel_us": kern, "copies": copies,
+            "inputs": (codes, scales, x)}
 
 
-def bench_gemv_bf16(torch, dev, steps, warmup):
+def bench_gemv_bf16(torch, lib, tm, dev, n):
     from iron_amd import _lib
     from oracle import configs
 
     M, K = 2048, 8192
     W, x = configs.cfg1_gemv_bf16(M=M, K=K)
-    nbytes = 2 * M * K + 2 * K + 2 * M  # 33,574,912 B
+    nbytes = 2 * M * K + 2 * K + 2 * M
     copies = max(2, POOL_BYTES // (2 * W.numel()))
     Ws = [W.to(dev) for _ in range(copies)]
     xd = x.to(dev)
     y = torch.empty(M, dtype=torch.bfloat16, device=dev)
     stream = _lib.stream_handle(dev)
-    lib = _lib.load()
-    fn = lib.iron_gemv_bf16
 
     def launch(i):
-        rc = fn(Ws[i % copies].data_ptr(), xd.data_ptr(), y.data_ptr(), M, K, 1, 0, stream)
-        if rc:
-            raise RuntimeError(lib.iron_last_error().decode())
+        _check(lib, lib.iron_gemv_bf16(Ws[i % copies].data_ptr(), xd.data_ptr(), y.data_ptr(), M, K, 1, 0, stream))
 
-    wall_ms, kern_us = time_steps(torch, launch, steps, warmup)
-    b2b_us = time_back_to_back(torch, launch, 200)
-    del Ws
-    return {"bytes": nbytes, "wall_ms": wall_ms, "kernel_us": kern_us, "b2b_us": b2b_us}
+    for i in range(20):
+        launch(i)
+    kern = tm.kernel_us(launch, n)
+    b2b = tm.wall_ms(launch, n) * 1e3 / n
+    return {"kernel_us": round(kern, 3), "GB/s": round(nbytes / kern / 1e3, 1),
+            "frac_hbm": round(nbytes / kern / 1e3 / HBM_PEAK_GBS, 4), "stream_us_per_launch": round(b2b, 3),
+            "algorithmic_bytes": nbytes}
 
 
-def cpu_baseline_int4(torch, inputs, budget_s=10.0):
-    """Oracle on the host cores: dequantize with torch ops, then matvec."""
+def bench_gqa(torch, lib, tm, dev, n):
+    from iron_amd import _lib
+    from oracle import configs
+
+    H, Hkv, D, L = 32, 8, 64, 2048
+    q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, head_dim=D, L=L)
+    nbytes = 2 * Hkv * L * D * 2 + H * D * 2 * 2 + 2 * Hkv * D * 2 + D * 4
+    copies = max(2, POOL_BYTES // (2 * kc.numel() * 2))
+    KC = [kc.to(dev) for _ in range(copies)]
+    VC = [vc.to(dev) for _ in range(copies)]
+    qd, knd, vnd, ad = q.to(dev), kn.to(dev), vn.to(dev), angles.to(dev)
+    out = torch.empty(H, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(int(lib.iron_gqa_decode_workspace_bytes(H, Hkv, D, L)), dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def launch(i):
+        _check(lib, lib.iron_gqa_decode(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), KC[i % copies].data_ptr(),
+                                        VC[i % copies].data_ptr(), ad.data_ptr(), L, out.data_ptr(), ws.data_ptr(),
+                                        H, Hkv, D, L, pos, None, 1.0 / math.sqrt(D), stream))
+
+    for i in range(20):
+        launch(i)
+    kern = tm.kernel_us(launch, n)
+    return {"kernel_us": round(kern, 3), "GB/s": round(nbytes / kern / 1e3, 1),
+            "frac_hbm": round(nbytes / kern / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+
+
+def bench_swiglu(torch, lib, tm, dev, n):
+    """Config 4: x + Wd(silu(Wg xn) * (Wu xn)), xn = RMSNorm(x)*w: two kernels
+    (norm + gate/up pair GEMV, then down GEMV + residual)."""
+    from iron_amd import _lib
+    from oracle import configs
+
+    E, F = 2048, 8192
+    x, nw, Wg, Wu, Wd = configs.cfg4_swiglu_block(E, F)
+    stream = _lib.stream_handle(dev)
+    xd, nwd = x.to(dev), nw.to(dev)
+    h = torch.empty(F, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(E, dtype=torch.bfloat16, device=dev)
+    res = {}
+    # bf16
+    g_, u_, d_ = Wg.to(dev), Wu.to(dev), Wd.to(dev)
+    reps = max(2, POOL_BYTES // (3 * 2 * E * F))
+    G = [g_] + [g_.clone() for _ in range(reps - 1)]
+    U = [u_] + [u_.clone() for _ in range(reps - 1)]
+    Dn = [d_] + [d_.clone() for _ in range(reps - 1)]
+
+    def up(i):
+        _check(lib, lib.iron_gemv_bf16_fused(G[i % reps].data_ptr(), U[i % reps].data_ptr(), xd.data_ptr(),
+                                             h.data_ptr(), F, E, 1, nwd.data_ptr(), 1e-5, None, 0, None, stream))
+
+    def down(i):
+        _check(lib, lib.iron_gemv_bf16_fused(Dn[i % reps].data_ptr(), None, h.data_ptr(), y.data_ptr(), E, F, 0,
+                                             None, 0.0, xd.data_ptr(), 0, None, stream))
+
+    for i in range(10):
+        up(i), down(i)
+    t = tm.kernel_us(up, n) + tm.kernel_us(down, n)
+    nbytes = 3 * 2 * E * F + 4 * E + 2 * 2 * F + 2 * E * 2
+    res["bf16"] = {"kernel_us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1),
+                   "frac_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    del G, U, Dn
+    # int4-g32
+    q = {}
+    for name, W in (("g", Wg), ("u", Wu), ("d", Wd)):
+        Wdv = W.to(dev)
+        c = torch.empty(W.shape[0], W.shape[1] // 2, dtype=torch.uint8, device=dev)
+        s = torch.empty(W.shape[0], W.shape[1] // 32, dtype=torch.bfloat16, device=dev)
+        _check(lib, lib.iron_quantize_i4g32(Wdv.data_ptr(), c.data_ptr(), s.data_ptr(), W.shape[0], W.shape[1],
+                                            stream))
+        q[name] = (c, s)
+    per = sum(c.numel() + 2 * s.numel() for c, s in q.values())
+    reps = max(2, POOL_BYTES // per)
+    Q = [q] + [{k: (c.clone(), s.clone()) for k, (c, s) in q.items()} for _ in range(reps - 1)]
+
+    def up4(i):
+        a = Q[i % reps]
+        _check(lib, lib.iron_gemv_i4g32_fused(a["g"][0].data_ptr(), a["g"][1].data_ptr(), a["u"][0].data_ptr(),
+                                              a["u"][1].data_ptr(), xd.data_ptr(), h.data_ptr(), F, E, 1, 1,
+                                              nwd.data_ptr(), 1e-5, None, 0, None, stream))
+
+    def down4(i):
+        a = Q[i % reps]
+        _check(lib, lib.iron_gemv_i4g32_fused(a["d"][0].data_ptr(), a["d"][1].data_ptr(), None, None, h.data_ptr(),
+                                              y.data_ptr(), E, F, 1, 0, None, 0.0, xd.data_ptr(), 0, None, stream))
+
+    for i in range(10):
+        up4(i), down4(i)
+    t = tm.kernel_us(up4, n) + tm.kernel_us(down4, n)
+    nbytes = per + 4 * E + 2 * 2 * F + 2 * E * 2
+    res["int4_g32"] = {"kernel_us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1),
+                       "frac_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    return res
+
+
+def bench_prefill_gemm(torch, lib, tm, dev, n):
+    from iron_amd import _lib
+
+    M, K, N = 512, 2048, 8192
+    g = torch.Generator(device=dev).manual_seed(0)
+    A = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+    W = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def launch(i):
+        _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+                                          stream))
+
+    for i in range(10):
+        launch(i)
+    t = tm.kernel_us(launch, n)
+    tf = 2.0 * M * N * K / t / 1e6
+    return {"shape": [M, K, N], "kernel_us": round(t, 3), "TFLOP/s": round(tf, 1),
+            "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
+def bench_model(torch, dev, decode_steps=128, prompt_len=512, long_ctx=3968):
+    """Config 5: random-init Llama-3.2-1B shape, int4-g32 linears, bf16 tied head."""
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
+
+    cfg = LlamaConfig(max_seq_len=long_ctx + decode_steps + 64)
+    t0 = time.perf_counter()
+    model = LlamaHIP(cfg, random_weights(cfg, dev, seed=0), device=dev)
+    init_s = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab_size, (prompt_len,), generator=g).tolist()
+    model.reset()
+    model.prefill(prompt)  # warm (code objects, buffers)
+    model.capture_decode_graph()
+    out = {"init_s": round(init_s, 2)}
+
+    model.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.prefill(prompt)
+    torch.cuda.synchronize()
+    ttft = time.perf_counter() - t0
+    out["prefill_tokens"] = prompt_len
+    out["ttft_ms"] = round(ttft * 1e3, 3)
+    out["prefill_tok_s"] = round(prompt_len / ttft, 1)
+
+    t0 = time.perf_counter()
+    model.decode(decode_steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out["decode_steps"] = decode_steps
+    out["decode_tok_s_kv512_640"] = round(decode_steps / dt, 1)
+    out["decode_ms_per_token_kv512_640"] = round(dt / decode_steps * 1e3, 4)
+
+    # long-context window: fill the cache to 3968, then decode to 4096
+    long_prompt = torch.randint(0, cfg.vocab_size, (long_ctx,), generator=g).tolist()
+    model.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.prefill(long_prompt)
+    torch.cuda.synchronize()
+    out["prefill_3968_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+    t0 = time.perf_counter()
+    model.decode(decode_steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out["decode_tok_s_kv3968_4096"] = round(decode_steps / dt, 1)
+    out["decode_ms_per_token_kv3968_4096"] = round(dt / decode_steps * 1e3, 4)
+    # bytes a decode token must stream at KV 4096 (int4 linears, bf16 head)
+    E, F, V, Lr = cfg.emb_dim, cfg.hidden_dim, cfg.vocab_size, cfg.n_layers
+    lin = (cfg.qkv_dim * E + E * E + 2 * F * E + E * F) * (0.5 + 2 / 32) * Lr
+    kv = 2 * cfg.n_kv_groups * 4096 * cfg.head_dim * 2 * Lr
+    head = V * E * 2
+    per_tok = lin + kv + head
+    out["decode_bytes_per_token_kv4096"] = int(per_tok)
+    out["decode_GB/s_kv3968_4096"] = round(per_tok * out["decode_tok_s_kv3968_4096"] / 1e9, 1)
+    out["decode_frac_hbm_kv3968_4096"] = round(out["decode_GB/s_kv3968_4096"] / HBM_PEAK_GBS, 4)
+    return out
+
+
+def cpu_baseline_int4(torch, inputs, budget_s):
+    """Oracle on the host cores: dequantize with torch ops, then fp32 matvec."""
     from oracle import ops
 
     codes, scales, x = inputs
@@ -155,7 +368,7 @@ def cpu_baseline_int4(torch, inputs, budget_s=10.0):
         "cores": threads,
         "kind": "port",
         "sample": f"{reps} x config-2 int4 GEMV (8192x2048) via oracle.ops.gemv_int4_reference "
-        f"(torch CPU dequant + fp32 matvec), {dt:.1f} s",
+        f"(torch CPU: dequantise to bf16, fp32 matvec), {dt:.1f} s",
     }
 
 
@@ -166,6 +379,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-model", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -181,13 +396,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    from iron_amd import _lib
+
+    lib = _lib.load()
     dev = torch.device("cuda", 0)
+    tm = Timer(torch, lib)
 
-    i4 = bench_gemv_int4(torch, dev, args.steps, args.warmup)
-    bf = bench_gemv_bf16(torch, dev, max(200, args.steps // 4), args.warmup)
-
+    i4 = bench_gemv_int4(torch, lib, tm, dev, args.steps, args.warmup)
     value = i4["bytes"] * args.steps / (i4["wall_ms"] * 1e-3) / 1e9
-    achieved = i4["bytes"] / (i4["kernel_us"] * 1e-6) / 1e9
+    achieved = i4["bytes"] / i4["kernel_us"] / 1e3
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -202,9 +419,9 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE configs[1]: fused int4-g32 dequant+GEMV, batch 1, W 8192x2048 "
-            "(signed int4, bf16 group-32 scales), x 2048 bf16, fp32 accumulate, bf16 out",
-            "weight_pool_copies": i4["pool_copies"],
+            "workload": "BASELINE configs[1]: fused int4-g32 dequant+GEMV, batch 1, W 8192x2048 (signed int4 "
+            "codes, bf16 group-32 scales, zero-point 0), x 2048 bf16 ~N(0,1), fp32 accumulate, bf16 out, seed 0",
+            "weight_pool_copies": i4["copies"],
             "algorithmic_bytes_per_step": i4["bytes"],
         },
         "roofline": {
@@ -214,19 +431,20 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "gemv_i4_kernel",
+            "kernel": "gemv_i4_fast<1, 2, false, false>",
             "kernel_us": round(i4["kernel_us"], 3),
         },
-        "extra": {
-            "gemv_bf16_cfg1": {
-                "kernel_us": round(bf["kernel_us"], 3),
-                "GB/s": round(bf["bytes"] / (bf["kernel_us"] * 1e-6) / 1e9, 1),
-                "frac_hbm": round(bf["bytes"] / (bf["kernel_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                "back_to_back_us_per_launch": round(bf["b2b_us"], 3),
-            },
-            "gemv_int4_cfg2_back_to_back_us_per_launch": round(i4["b2b_us"], 3),
-        },
     }
+    if not args.no_extra:
+        extra = {
+            "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300),
+            "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
+            "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200),
+            "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+        }
+        if not args.no_model:
+            extra["llama_cfg5"] = bench_model(torch, dev)
+        out["extra"] = extra
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_int4(torch, i4["inputs"], args.cpu_seconds)
     print(json.dumps(out), flush=True)

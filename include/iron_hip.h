@@ -29,6 +29,15 @@ extern "C" {
 const char* iron_last_error(void);
 int iron_abi_version(void);
 
+/* Instrumentation: arm two hipEvent_t (created with timing enabled) for the
+ * calling thread's next entry-point call: its kernels record start_event at
+ * the first kernel's start and stop_event at the last kernel's end
+ * (hipExtLaunchKernel), so their elapsed time is the call's device execution
+ * time without the host dispatch before it -- the analogue of the per-dispatch
+ * device time the reference benchmarks report (iron/common/test_utils.py:
+ * 216-219). Disarmed after that call; NULL, NULL disarms. Results unchanged. */
+int iron_time_next_launch(void* start_event, void* stop_event);
+
 /* Epilogue codes shared by GEMV and GEMM. GELU_TANH is the tanh approximation
  * of iron/operators/gemv/reference.py:69-76; GELU_SIGMOID is x*sigmoid(1.702x)
  * of iron/operators/flm/gemm/reference.py:8-31. */
@@ -50,15 +59,27 @@ enum iron_epilogue {
 int iron_gemv_bf16(const void* W, const void* x, void* y, int M, int K, int batches, int epilogue,
                    void* stream);
 
+/* RMSNorm modes of the fused GEMVs. */
+enum iron_norm_mode {
+  IRON_NORM_NONE = 0,   /* x used as given */
+  IRON_NORM_WEIGHT = 1, /* x -> bf16(x * rsqrt(mean(x^2)+eps) * norm_w), the reference order */
+  IRON_NORM_SCALE = 2   /* output rows * rsqrt(mean(x^2)+eps); the norm weight is folded into
+                           the matrix columns beforehand (W' = W diag(norm_w)) */
+};
+
 /* Decode-step GEMV with optional fusions (NULL disables each):
- *   norm_w   (K,)  : x is replaced by bf16(x * rsqrt(mean(x^2)+eps) * norm_w)
- *   W2       (M,K) : output is silu(W.x) * (W2.x)  (epilogue must be NONE)
- *   residual (M,)  : added before the final bf16 rounding (may alias y)
+ *   norm_mode/norm_w : RMSNorm of x (enum iron_norm_mode; norm_w only for mode 1)
+ *   W2 (M,K)         : output is silu(W.x) * (W2.x)  (epilogue must be NONE)
+ *   residual (M,)    : added before the final bf16 rounding (may alias y)
+ *   argmax_keys      : uint64 per 4 output rows (ceil(M/4) of them): the
+ *                      largest (value, -row) key of those rows, for
+ *                      iron_argmax_select (greedy sampling without a scan)
  * Fuses the RMSNorm -> GEMV and GEMV -> ElementwiseAdd / SiLU -> Mul steps of
  * the decode runlist iron/applications/llama_3.2_1b/llama_npu.py:459-557 and
  * the SwiGLUDecode sequence iron/operators/swiglu_decode/op.py:56-62. */
-int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x, void* y, int M, int K,
-                         const void* norm_w, float eps, const void* residual, int epilogue, void* stream);
+int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x, void* y, int M, int K, int norm_mode,
+                         const void* norm_w, float eps, const void* residual, int epilogue, void* argmax_keys,
+                         void* stream);
 
 /* Fused int4 dequant + GEMV, group 32: codes (M,K/2) uint8 (two weights per
  * byte along K, low nibble first), scales (M,K/32) bf16, zero-point 0.
@@ -70,8 +91,8 @@ int iron_gemv_i4g32(const void* codes, const void* scales, const void* x, void* 
 
 /* int4 counterpart of iron_gemv_bf16_fused (codes2/scales2 = SwiGLU up). */
 int iron_gemv_i4g32_fused(const void* codes, const void* scales, const void* codes2, const void* scales2,
-                          const void* x, void* y, int M, int K, int is_signed, const void* norm_w, float eps,
-                          const void* residual, int epilogue, void* stream);
+                          const void* x, void* y, int M, int K, int is_signed, int norm_mode, const void* norm_w,
+                          float eps, const void* residual, int epilogue, void* argmax_keys, void* stream);
 
 /* ------------------------------------------------------------- Dequant ---- */
 
@@ -144,8 +165,8 @@ int iron_rope(const void* x, const void* angles, int angles_fp32, void* out, int
 /* ----------------------------------------------------------- Attention ---- */
 
 /* Bytes of workspace iron_gqa_decode needs for this shape (-1 if invalid).
- * The first 256 bytes are ticket counters: zero them once after allocation;
- * every call leaves them zero again. */
+ * Scratch for the per-chunk partial results (no initialisation needed); calls
+ * that share one workspace must be stream-ordered. */
 long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
 
 /* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}):
@@ -207,6 +228,14 @@ int iron_embedding(const void* table, const int* ids, void* out, int n, int dim,
  * loop on the GPU (the harness samples on the CPU:
  * iron/applications/llama_3.2_1b/llama_inference_harness.py:146-169). */
 int iron_argmax_bf16(const void* x, int n, int* token_out, int* pos, int* history, int history_cap, void* stream);
+
+/* Greedy selection from GEMV argmax keys (iron_gemv_*_fused argmax_keys):
+ * token_out[0] = row of the largest key; when pos is given, history[*pos] =
+ * token (if *pos < history_cap) and *pos += 1; when table is given, x_out =
+ * table[token] (dim bf16). One workgroup; replaces the full-vocabulary scan of
+ * iron_argmax_bf16 in the decode loop and fuses the next token's embedding. */
+int iron_argmax_select(const void* keys, int n_keys, const void* table, int dim, int vocab, void* x_out,
+                       int* token_out, int* pos, int* history, int history_cap, void* stream);
 
 /* Prefill scatter: qkv (seq, (H+2Hkv)*64) -> q_out (seq, H*64) rotated,
  * k_cache[:, pos0+s] rotated, v_cache[:, pos0+s] = v (two-halves RoPE with

@@ -24,10 +24,11 @@ _LL = ctypes.c_longlong
 
 # name -> argtypes (every function returns int, 0 = success) ...
 SIGNATURES: dict[str, list] = {
+    "iron_time_next_launch": [_P, _P],
     "iron_gemv_bf16": [_P, _P, _P, _I, _I, _I, _I, _P],
-    "iron_gemv_bf16_fused": [_P, _P, _P, _P, _I, _I, _P, _F, _P, _I, _P],
+    "iron_gemv_bf16_fused": [_P, _P, _P, _P, _I, _I, _I, _P, _F, _P, _I, _P, _P],
     "iron_gemv_i4g32": [_P, _P, _P, _P, _I, _I, _I, _P],
-    "iron_gemv_i4g32_fused": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _F, _P, _I, _P],
+    "iron_gemv_i4g32_fused": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _F, _P, _I, _P, _P],
     "iron_dequant_i4": [_P, _P, _P, _I, _I, _I, _I, _P],
     "iron_dequant_i4_payload": [_P, _P, _LL, _I, _I, _I, _P],
     "iron_rmsnorm": [_P, _P, _P, _P, _P, _I, _I, _F, _P],
@@ -45,6 +46,7 @@ SIGNATURES: dict[str, list] = {
     "iron_quantize_i4g32": [_P, _P, _P, _I, _I, _P],
     "iron_embedding": [_P, _P, _P, _I, _I, _I, _P],
     "iron_argmax_bf16": [_P, _I, _P, _P, _P, _I, _P],
+    "iron_argmax_select": [_P, _I, _P, _I, _I, _P, _P, _P, _P, _I, _P],
     "iron_qkv_rope_scatter": [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
 }
 

@@ -1,22 +1,23 @@
 """Llama-3.2-1B on MI355X: the reference application's forward pass
 (iron/applications/llama_3.2_1b/llama_npu.py) rebuilt on the HIP kernels.
 
-Decode (one token) is 5 kernels per layer plus 3, all reading the token id and
+Decode (one token) is 6 kernels per layer plus 2, all reading the token id and
 position from device memory:
 
-    embedding(token)                                     iron_embedding
+    token = argmax(keys); pos += 1; x = emb[token]       iron_argmax_select
     per layer:
-      qkv = Wqkv . rmsnorm(x)                            iron_gemv_i4g32_fused (norm fused)
-      attn = gqa(rope(q), rope(k) -> cache, v -> cache)  iron_gqa_decode (split-K, pos on device)
+      qkv = Wqkv' . x * inv_rms(x)                       iron_gemv_i4g32_fused (norm fused)
+      attn = gqa(rope(q), rope(k) -> cache, v -> cache)  iron_gqa_decode (split-K + merge)
       x  += Wo . attn                                    iron_gemv_i4g32_fused (residual fused)
-      h   = silu(Wg . rmsnorm(x)) * (Wu . rmsnorm(x))    iron_gemv_i4g32_fused (pair + norm)
+      h   = silu(Wg' . x * r) * (Wu' . x * r)            iron_gemv_i4g32_fused (pair + norm)
       x  += Wd . h                                       iron_gemv_i4g32_fused (residual fused)
-    logits = Wemb . rmsnorm(x)                           iron_gemv_bf16_fused (tied head)
-    token, pos += 1                                      iron_argmax_bf16
+    logits = Whead' . x * inv_rms(x), argmax keys        iron_gemv_bf16_fused
 
 so the step is captured once as a HIP graph and replayed for every token with
 no host synchronisation (the reference's single fused decode dispatch,
-llama_npu.py:459-584, is the analogue). Prefill runs the same layers on bf16
+llama_npu.py:459-584, is the analogue). Each RMSNorm weight is folded into the
+columns of the matrix that consumes the normalised vector (W' = W diag(w)),
+so the GEMVs only scale their outputs by rsqrt(mean(x^2) + eps). Prefill runs the same layers on bf16
 MFMA GEMMs over the prompt (iron_gemm_bf16_nt) with causal flash attention
 (iron_attention_prefill), replacing the reference's GEMM + CPU-softmax path
 (llama_npu.py:1028-1149).
@@ -150,16 +151,20 @@ class Linear:
             self.bf16 = weight.contiguous()
         self.int4 = int4
 
-    def gemv(self, x, y, stream, norm_w=None, eps=0.0, residual=None, pair: "Linear | None" = None):
-        """y = [silu](W . norm(x)) [* (W2 . norm(x))] [+ residual] on one token."""
+    def gemv(self, x, y, stream, norm_scale=False, eps=0.0, residual=None, pair: "Linear | None" = None,
+             keys=None):
+        """y = [silu](W . x * r) [* (W2 . x * r)] [+ residual] on one token, with
+        r = rsqrt(mean(x^2) + eps) when norm_scale (norm weight folded into W)."""
+        mode = 2 if norm_scale else 0
         if self.int4:
             _lib.call("iron_gemv_i4g32_fused", self.codes.data_ptr(), self.scales.data_ptr(),
                       _lib.ptr(pair.codes if pair else None), _lib.ptr(pair.scales if pair else None), x.data_ptr(),
-                      y.data_ptr(), self.N, self.K, 1, _lib.ptr(norm_w), float(eps), _lib.ptr(residual), 0, stream)
+                      y.data_ptr(), self.N, self.K, 1, mode, None, float(eps), _lib.ptr(residual), 0, _lib.ptr(keys),
+                      stream)
         else:
             _lib.call("iron_gemv_bf16_fused", self.bf16.data_ptr(), _lib.ptr(pair.bf16 if pair else None),
-                      x.data_ptr(), y.data_ptr(), self.N, self.K, _lib.ptr(norm_w), float(eps), _lib.ptr(residual),
-                      0, stream)
+                      x.data_ptr(), y.data_ptr(), self.N, self.K, mode, None, float(eps), _lib.ptr(residual), 0,
+                      _lib.ptr(keys), stream)
 
     def gemm(self, X, Y, rows, stream):
         """Y (rows, N) = X (rows, K) . W^T on bf16 MFMA."""
@@ -179,21 +184,26 @@ class LlamaHIP:
         E, Hd = cfg.emb_dim, cfg.head_dim
         dev = self.device
         w = {k: v.to(dev, BF16).contiguous() for k, v in weights.items()}
+
+        def fold(W, norm):  # W diag(norm): the norm weight moves into the matrix columns
+            return (W.float() * norm.float().unsqueeze(0)).to(BF16)
+
         self.embed = w["model.embed_tokens.weight"]
         self.final_norm = w["model.norm.weight"]
-        self.head = Linear(self.embed, cfg.head_int4, s) if cfg.head_int4 else None
+        self.head = Linear(fold(self.embed, self.final_norm), cfg.head_int4, s)
         self.layers = []
         for i in range(cfg.n_layers):
             p = f"model.layers.{i}."
+            an, fn = w[p + "input_layernorm.weight"], w[p + "post_attention_layernorm.weight"]
             qkv = torch.cat([w[p + "self_attn.q_proj.weight"], w[p + "self_attn.k_proj.weight"],
                              w[p + "self_attn.v_proj.weight"]], dim=0)
             self.layers.append({
-                "attn_norm": w[p + "input_layernorm.weight"],
-                "ffn_norm": w[p + "post_attention_layernorm.weight"],
-                "qkv": Linear(qkv, cfg.int4, s),
+                "attn_norm": an,
+                "ffn_norm": fn,
+                "qkv": Linear(fold(qkv, an), cfg.int4, s),
                 "o": Linear(w[p + "self_attn.o_proj.weight"], cfg.int4, s),
-                "gate": Linear(w[p + "mlp.gate_proj.weight"], cfg.int4, s),
-                "up": Linear(w[p + "mlp.up_proj.weight"], cfg.int4, s),
+                "gate": Linear(fold(w[p + "mlp.gate_proj.weight"], fn), cfg.int4, s),
+                "up": Linear(fold(w[p + "mlp.up_proj.weight"], fn), cfg.int4, s),
                 "down": Linear(w[p + "mlp.down_proj.weight"], cfg.int4, s),
             })
         del w
@@ -211,6 +221,8 @@ class LlamaHIP:
         self.logits = torch.zeros(cfg.vocab_size, dtype=BF16, device=dev)
         self.xn = torch.zeros(E, dtype=BF16, device=dev)
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.n_keys = (cfg.vocab_size + 3) // 4
+        self.keys = torch.zeros(self.n_keys, dtype=torch.int64, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.history = torch.zeros(L, dtype=torch.int32, device=dev)
         self.host_pos = 0
@@ -223,22 +235,29 @@ class LlamaHIP:
         return _lib.stream_handle(self.device)
 
     def effective_weights(self) -> dict:
-        """The weights the model computes with (dequantised int4 as bf16), HF names."""
+        """Weights the model computes with, as fp32 in the reference's layout (HF
+        names): the int4-g32 dequantised matrices with the folded norm weights
+        divided back out, the norms, and an untied ``lm_head.weight``."""
         cfg = self.cfg
         q_rows, kv_rows = cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
-        out = {"model.embed_tokens.weight": self.embed, "model.norm.weight": self.final_norm}
+
+        def unfold(W, norm):
+            return W.float() / norm.float().unsqueeze(0)
+
+        out = {"model.embed_tokens.weight": self.embed.float(), "model.norm.weight": self.final_norm.float(),
+               "lm_head.weight": unfold(self.head.bf16, self.final_norm)}
         for i, L in enumerate(self.layers):
             p = f"model.layers.{i}."
-            qkv = L["qkv"].bf16
+            qkv = unfold(L["qkv"].bf16, L["attn_norm"])
             out[p + "self_attn.q_proj.weight"] = qkv[:q_rows]
             out[p + "self_attn.k_proj.weight"] = qkv[q_rows : q_rows + kv_rows]
             out[p + "self_attn.v_proj.weight"] = qkv[q_rows + kv_rows :]
-            out[p + "self_attn.o_proj.weight"] = L["o"].bf16
-            out[p + "mlp.gate_proj.weight"] = L["gate"].bf16
-            out[p + "mlp.up_proj.weight"] = L["up"].bf16
-            out[p + "mlp.down_proj.weight"] = L["down"].bf16
-            out[p + "input_layernorm.weight"] = L["attn_norm"]
-            out[p + "post_attention_layernorm.weight"] = L["ffn_norm"]
+            out[p + "self_attn.o_proj.weight"] = L["o"].bf16.float()
+            out[p + "mlp.gate_proj.weight"] = unfold(L["gate"].bf16, L["ffn_norm"])
+            out[p + "mlp.up_proj.weight"] = unfold(L["up"].bf16, L["ffn_norm"])
+            out[p + "mlp.down_proj.weight"] = L["down"].bf16.float()
+            out[p + "input_layernorm.weight"] = L["attn_norm"].float()
+            out[p + "post_attention_layernorm.weight"] = L["ffn_norm"].float()
         return out
 
     def reset(self) -> None:
@@ -248,31 +267,35 @@ class LlamaHIP:
 
     # ------------------------------------------------------------ decode
     def decode_step(self) -> None:
-        """Enqueue one decode step: token/pos from device memory, next token and pos+1 back."""
+        """Enqueue one decode step: the previous step's argmax keys pick the token
+        (pos advances), then the layers, then the head writes logits and keys."""
         cfg, s = self.cfg, self._stream()
         Hd, q_rows, kv_rows = cfg.head_dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
-        _lib.call("iron_embedding", self.embed.data_ptr(), self.token.data_ptr(), self.x.data_ptr(), 1, cfg.emb_dim,
-                  cfg.vocab_size, s)
+        _lib.call("iron_argmax_select", self.keys.data_ptr(), self.n_keys, self.embed.data_ptr(), cfg.emb_dim,
+                  cfg.vocab_size, self.x.data_ptr(), self.token.data_ptr(), self.pos.data_ptr(),
+                  self.history.data_ptr(), cfg.max_seq_len, s)
         q = self.qkv[:q_rows]
         k = self.qkv[q_rows : q_rows + kv_rows]
         v = self.qkv[q_rows + kv_rows :]
         scale = 1.0 / math.sqrt(Hd)
         for i, L in enumerate(self.layers):
-            L["qkv"].gemv(self.x, self.qkv, s, norm_w=L["attn_norm"], eps=cfg.eps)
+            L["qkv"].gemv(self.x, self.qkv, s, norm_scale=True, eps=cfg.eps)
             _lib.call("iron_gqa_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), self.angles.data_ptr(), self.angles.shape[0], self.attn.data_ptr(),
                       self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, 0,
                       self.pos.data_ptr(), scale, s)
             L["o"].gemv(self.attn, self.x, s, residual=self.x)
-            L["gate"].gemv(self.x, self.h, s, norm_w=L["ffn_norm"], eps=cfg.eps, pair=L["up"])
+            L["gate"].gemv(self.x, self.h, s, norm_scale=True, eps=cfg.eps, pair=L["up"])
             L["down"].gemv(self.h, self.x, s, residual=self.x)
-        if self.head is not None:
-            self.head.gemv(self.x, self.logits, s, norm_w=self.final_norm, eps=cfg.eps)
-        else:
-            _lib.call("iron_gemv_bf16_fused", self.embed.data_ptr(), None, self.x.data_ptr(), self.logits.data_ptr(),
-                      cfg.vocab_size, cfg.emb_dim, self.final_norm.data_ptr(), float(cfg.eps), None, 0, s)
-        _lib.call("iron_argmax_bf16", self.logits.data_ptr(), cfg.vocab_size, self.token.data_ptr(),
-                  self.pos.data_ptr(), self.history.data_ptr(), cfg.max_seq_len, s)
+        self.head.gemv(self.x, self.logits, s, norm_scale=True, eps=cfg.eps, keys=self.keys)
+
+    def commit(self) -> None:
+        """Record the token chosen by the last logits (history[pos], pos += 1)
+        without starting a step."""
+        cfg = self.cfg
+        _lib.call("iron_argmax_select", self.keys.data_ptr(), self.n_keys, None, cfg.emb_dim, cfg.vocab_size, None,
+                  self.token.data_ptr(), self.pos.data_ptr(), self.history.data_ptr(), cfg.max_seq_len,
+                  self._stream())
 
     def _warmup(self) -> None:
         """Run every decode kernel once eagerly (code objects load before capture).
@@ -280,12 +303,12 @@ class LlamaHIP:
         Uses the last cache slot, which a later step at that position rewrites
         before any attention reads it; token and position are restored.
         """
-        tok = self.token.clone()
-        pos = self.pos.clone()
+        tok, pos, keys = self.token.clone(), self.pos.clone(), self.keys.clone()
         self.pos.fill_(self.cfg.max_seq_len - 1)
         self.decode_step()
         self.token.copy_(tok)
         self.pos.copy_(pos)
+        self.keys.copy_(keys)
         torch.cuda.synchronize(self.device)
 
     def capture_decode_graph(self) -> None:
@@ -352,13 +375,13 @@ class LlamaHIP:
         scale = 1.0 / math.sqrt(Hd)
         first = True
         for i, L in enumerate(self.layers):
+            # norm weights are folded into the next matrices: unweighted RMSNorm
             if first:
-                _lib.call("iron_rmsnorm", X.data_ptr(), None, L["attn_norm"].data_ptr(), Xn.data_ptr(), None, S, E,
-                          float(cfg.eps), s)
+                _lib.call("iron_rmsnorm", X.data_ptr(), None, None, Xn.data_ptr(), None, S, E, float(cfg.eps), s)
                 first = False
             else:  # X += T (previous FFN output), Xn = norm(X)
-                _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), L["attn_norm"].data_ptr(), Xn.data_ptr(),
-                          X.data_ptr(), S, E, float(cfg.eps), s)
+                _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
+                          float(cfg.eps), s)
             L["qkv"].gemm(Xn, b["QKV"], S, s)
             _lib.call("iron_qkv_rope_scatter", b["QKV"].data_ptr(), self.angles.data_ptr(), self.angles.shape[0],
                       b["Q"].data_ptr(), self.k_cache[i].data_ptr(), self.v_cache[i].data_ptr(), S, cfg.n_heads,
@@ -367,28 +390,23 @@ class LlamaHIP:
                       self.v_cache[i].data_ptr(), b["O"].data_ptr(), cfg.n_heads, cfg.n_kv_groups, S, pos0 + S, Hd,
                       Hd, cfg.n_heads * Hd, cfg.max_seq_len * Hd, Hd, Hd, cfg.n_heads * Hd, S, 1, pos0, scale, s)
             L["o"].gemm(b["O"], T, S, s)
-            _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), L["ffn_norm"].data_ptr(), Xn.data_ptr(),
-                      X.data_ptr(), S, E, float(cfg.eps), s)
+            _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
+                      float(cfg.eps), s)
             L["gate"].gemm(Xn, b["G"], S, s)
             L["up"].gemm(Xn, b["U"], S, s)
             _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(), S * cfg.hidden_dim, s)
             L["down"].gemm(b["G"], T, S, s)
-        _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), self.final_norm.data_ptr(), Xn.data_ptr(),
-                  X.data_ptr(), S, E, float(cfg.eps), s)
-        last = Xn[S - 1]
-        if self.head is not None:
-            self.head.gemv(last, self.logits, s)
-        else:
-            _lib.call("iron_gemv_bf16", self.embed.data_ptr(), last.data_ptr(), self.logits.data_ptr(),
-                      cfg.vocab_size, E, 1, 0, s)
+        _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
+                  float(cfg.eps), s)
+        self.head.gemv(Xn[S - 1], self.logits, s, keys=self.keys)
         self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
-        _lib.call("iron_argmax_bf16", self.logits.data_ptr(), cfg.vocab_size, self.token.data_ptr(),
-                  self.pos.data_ptr(), self.history.data_ptr(), cfg.max_seq_len, s)
         self.host_pos = pos0 + S
 
     def set_token(self, token: int) -> None:
-        """Override the next input token (teacher forcing)."""
-        self.token.copy_(torch.tensor([int(token)], dtype=torch.int32))
+        """Force the next input token (teacher forcing): the next step's selection
+        picks it regardless of the logits."""
+        forced = (0xFFFFFFFF << 32) | (0xFFFFFFFF - int(token))  # above every logit's key (unsigned order)
+        self.keys[:1].copy_(torch.tensor([forced - (1 << 64)], dtype=torch.int64))  # same bits as int64
 
     def generate(self, prompt_ids, n_tokens: int, use_graph: bool = True) -> list[int]:
         """Greedy generation: prefill the prompt, then n_tokens-1 decode steps.
@@ -398,5 +416,6 @@ class LlamaHIP:
         S = self.host_pos
         if n_tokens > 1:
             self.decode(n_tokens - 1, use_graph=use_graph)
+        self.commit()
         torch.cuda.synchronize(self.device)
         return self.history[S - 1 : S - 1 + n_tokens].tolist()

@@ -4,9 +4,10 @@
 // positions) and serves the G = H/Hkv query heads that share KV head j, so
 // every K/V byte is read from HBM once for all of them. Inside the chunk the
 // softmax is exact in fp32 (scores scaled by log2(e)/sqrt(D), exp2); the
-// chunk's unnormalised output, maximum and sum go to a workspace. The last
-// workgroup of a KV head to finish (ticket counter, reset by that workgroup)
-// merges the chunks: no second launch and no spin-waiting.
+// chunk's unnormalised output, maximum and sum go to a workspace, and a second
+// small kernel merges the chunks. (Merging in the last-arriving workgroup
+// would need an agent-scope fence per workgroup, which on this GPU writes back
+// and invalidates the whole per-XCD L2: far dearer than one more launch.)
 // RoPE for q and the new k is applied on load (two-halves rotation, row `pos`
 // of an fp32 [cos, sin] interleaved table, result rounded to bf16 as the RoPE
 // operator does), and the new k/v are written into the caches at `pos` by the
@@ -33,7 +34,6 @@ struct DecodeArgs {
   const float* angles;    // (angle_rows, D) [cos0, sin0, cos1, sin1, ...]
   uint16_t* out;          // (H, D)
   float* part;            // (Hkv, nsplit, G*D + 2G) partials
-  int* counters;          // (Hkv,) zero on entry, zero on exit
   const int* pos_dev;     // optional device-resident position (overrides pos)
   int pos;
   int max_len;
@@ -55,13 +55,6 @@ __device__ __forceinline__ void rope_pair_lds(float* v, const float* ang, int i)
   v[i + 32] = bf16_to_f32(f32_to_bf16(x2 * c + x1 * s));
 }
 
-__device__ __forceinline__ float ld_coherent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int G>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
@@ -72,7 +65,6 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   __shared__ float vn_s[D];
   __shared__ float red_s[NW][G];
   __shared__ float o_s[G][kDecThreads / 8][D];  // per (head, position row, dim)
-  __shared__ int ticket_s;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int s = blockIdx.x, j = blockIdx.y;
@@ -80,7 +72,6 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * kDecChunk;
-  const int nact = (L + kDecChunk - 1) / kDecChunk;
   float* part = a.part + (static_cast<size_t>(j) * a.nsplit + s) * PS;
 
   if (p0 < L) {
@@ -189,37 +180,99 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
       float acc = 0.f;
 #pragma unroll 8
       for (int rr = 0; rr < kDecThreads / 8; ++rr) acc += o_s[g][rr][d];
-      st_coherent(part + t, acc);
+      part[t] = acc;
     }
     if (tid < G) {
       float l = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) l += red_s[w][tid];
-      st_coherent(part + G * D + tid, mloc[tid]);
-      st_coherent(part + G * D + G + tid, l);
+      part[G * D + tid] = mloc[tid];
+      part[G * D + G + tid] = l;
     }
   }
 
-  // Ticket: the last workgroup of this KV head merges the active chunks.
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) ticket_s = atomicAdd(a.counters + j, 1);
-  __syncthreads();
-  if (ticket_s != a.nsplit - 1) return;
-  __threadfence();
-  if (tid == 0) a.counters[j] = 0;  // every other workgroup has already taken its ticket
+}
+
+// Merge of the chunk partials of one KV head (one workgroup per KV head).
+template <int G>
+__global__ __launch_bounds__(kDecThreads) void gqa_combine_kernel(DecodeArgs a) {
+  constexpr int D = kD;
+  constexpr int NW = kDecThreads / kWave;
+  constexpr int PS = part_stride<G>();
+  __shared__ float red_s[NW][G];
+  __shared__ float w_s[kDecThreads * G];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int j = blockIdx.x;
+  const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+  if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
+  const int nact = (pos + kDecChunk) / kDecChunk;
   const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
-  for (int t = tid; t < G * D; t += kDecThreads) {
-    const int g = t / D;
-    float M = -INFINITY;
-    for (int k = 0; k < nact; ++k) M = fmaxf(M, ld_coherent(base + k * PS + G * D + g));
-    float lt = 0.f, o = 0.f;
-    for (int k = 0; k < nact; ++k) {
-      const float w = exp2f(ld_coherent(base + k * PS + G * D + g) - M);
-      lt = fmaf(ld_coherent(base + k * PS + G * D + G + g), w, lt);
-      o = fmaf(ld_coherent(base + k * PS + t), w, o);
+  // global maximum and sum per head: splits strided over the threads
+  float mg[G], lg[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) mg[g] = -INFINITY;
+  for (int k = tid; k < nact; k += kDecThreads)
+#pragma unroll
+    for (int g = 0; g < G; ++g) mg[g] = fmaxf(mg[g], base[k * PS + G * D + g]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = wave_max(mg[g]);
+    if (lane == 0) red_s[wave][g] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = red_s[0][g];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, red_s[w][g]);
+    mg[g] = m;
+    lg[g] = 0.f;
+  }
+  __syncthreads();
+  for (int k = tid; k < nact; k += kDecThreads)
+#pragma unroll
+    for (int g = 0; g < G; ++g) lg[g] += base[k * PS + G * D + G + g] * exp2f(base[k * PS + G * D + g] - mg[g]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float l = wave_sum(lg[g]);
+    if (lane == 0) red_s[wave][g] = l;
+  }
+  __syncthreads();
+  float inv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) l += red_s[w][g];
+    inv[g] = 1.f / l;
+  }
+  // outputs: per-split weights staged in LDS (slabs of kDecThreads splits),
+  // partial outputs read as independent loads
+  constexpr int OPT = (G * D + kDecThreads - 1) / kDecThreads;  // outputs per thread
+  float acc[OPT];
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) acc[i] = 0.f;
+  for (int k0 = 0; k0 < nact; k0 += kDecThreads) {
+    const int kn = min(kDecThreads, nact - k0);
+    __syncthreads();
+    if (tid < kn)
+#pragma unroll
+      for (int g = 0; g < G; ++g) w_s[tid * G + g] = exp2f(base[(k0 + tid) * PS + G * D + g] - mg[g]);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < OPT; ++i) {
+      const int t = tid + i * kDecThreads, g = t / D;
+      if (t >= G * D) break;
+      float o = acc[i];
+#pragma unroll 8
+      for (int k = 0; k < kn; ++k) o = fmaf(base[(k0 + k) * PS + t], w_s[k * G + g], o);
+      acc[i] = o;
     }
-    a.out[static_cast<size_t>(j) * G * D + t] = f32_to_bf16(o / lt);
+  }
+#pragma unroll
+  for (int i = 0; i < OPT; ++i) {
+    const int t = tid + i * kDecThreads, g = t / D;
+    if (t < G * D) a.out[static_cast<size_t>(j) * G * D + t] = f32_to_bf16(acc[i] * inv[g]);
   }
 }
 
@@ -375,7 +428,7 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim != kD || max_len <= 0) return -1;
   const int G = n_heads / n_kv_heads;
   const long long part = static_cast<long long>(n_kv_heads) * decode_nsplit(max_len) * (G * kD + 2 * G) * 4;
-  return 256 + part;  // counters (zeroed by the caller once), then partials
+  return 256 + part;  // 256 reserved bytes, then partials
 }
 
 extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -404,7 +457,6 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
   a.v_cache = static_cast<uint16_t*>(v_cache);
   a.angles = angles;
   a.out = static_cast<uint16_t*>(out);
-  a.counters = static_cast<int*>(workspace);
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
   a.pos_dev = pos_dev;
   a.pos = pos;
@@ -414,11 +466,24 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
   a.scale_log2 = scale * 1.4426950408889634f;
   dim3 grid(a.nsplit, n_kv_heads), block(kDecThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 cgrid(n_kv_heads);
   switch (G) {
-    case 1: hipLaunchKernelGGL((gqa_decode_kernel<1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((gqa_decode_kernel<2>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((gqa_decode_kernel<4>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((gqa_decode_kernel<8>), grid, block, 0, s, a); break;
+    case 1:
+      IRON_LAUNCH((gqa_decode_kernel<1>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<1>), cgrid, block, 0, s, a);
+      break;
+    case 2:
+      IRON_LAUNCH((gqa_decode_kernel<2>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<2>), cgrid, block, 0, s, a);
+      break;
+    case 4:
+      IRON_LAUNCH((gqa_decode_kernel<4>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<4>), cgrid, block, 0, s, a);
+      break;
+    default:
+      IRON_LAUNCH((gqa_decode_kernel<8>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, block, 0, s, a);
+      break;
   }
   return check_launch("gqa_decode");
 }
@@ -459,6 +524,6 @@ extern "C" int iron_attention_prefill(const void* q, const void* k, const void* 
                 q_offset,
                 scale * 1.4426950408889634f};
   dim3 grid((out_rows + kPfQ - 1) / kPfQ, n_heads), block(256);
-  hipLaunchKernelGGL(attention_prefill_kernel, grid, block, 0, static_cast<hipStream_t>(stream), a);
+  IRON_LAUNCH(attention_prefill_kernel, grid, block, 0, static_cast<hipStream_t>(stream), a);
   return check_launch("attention_prefill");
 }

@@ -243,11 +243,11 @@ int ew_launch(int op, const void* a, const void* b, void* out, long long n, hipS
   auto* O = static_cast<uint16_t*>(out);
   dim3 g(static_cast<unsigned>(blocks)), blk(kBlock);
   switch (op) {
-    case EW_ADD: hipLaunchKernelGGL((eltwise_kernel<EW_ADD>), g, blk, 0, s, A, B, O, n); break;
-    case EW_MUL: hipLaunchKernelGGL((eltwise_kernel<EW_MUL>), g, blk, 0, s, A, B, O, n); break;
-    case EW_SILU: hipLaunchKernelGGL((eltwise_kernel<EW_SILU>), g, blk, 0, s, A, B, O, n); break;
-    case EW_SILU_MUL: hipLaunchKernelGGL((eltwise_kernel<EW_SILU_MUL>), g, blk, 0, s, A, B, O, n); break;
-    default: hipLaunchKernelGGL((eltwise_kernel<EW_GELU_TANH>), g, blk, 0, s, A, B, O, n); break;
+    case EW_ADD: IRON_LAUNCH((eltwise_kernel<EW_ADD>), g, blk, 0, s, A, B, O, n); break;
+    case EW_MUL: IRON_LAUNCH((eltwise_kernel<EW_MUL>), g, blk, 0, s, A, B, O, n); break;
+    case EW_SILU: IRON_LAUNCH((eltwise_kernel<EW_SILU>), g, blk, 0, s, A, B, O, n); break;
+    case EW_SILU_MUL: IRON_LAUNCH((eltwise_kernel<EW_SILU_MUL>), g, blk, 0, s, A, B, O, n); break;
+    default: IRON_LAUNCH((eltwise_kernel<EW_GELU_TANH>), g, blk, 0, s, A, B, O, n); break;
   }
   return check_launch("eltwise");
 }
@@ -277,10 +277,10 @@ extern "C" int iron_rmsnorm(const void* x, const void* residual, const void* w, 
   auto O = static_cast<uint16_t*>(out);
   auto S = static_cast<uint16_t*>(sum_out);
   dim3 g(rows), b(kBlock);
-  if (cpt <= 1) hipLaunchKernelGGL((rmsnorm_kernel<1>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else if (cpt <= 2) hipLaunchKernelGGL((rmsnorm_kernel<2>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else if (cpt <= 4) hipLaunchKernelGGL((rmsnorm_kernel<4>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else hipLaunchKernelGGL((rmsnorm_kernel<8>), g, b, 0, s, X, R, W, O, S, cols, eps);
+  if (cpt <= 1) IRON_LAUNCH((rmsnorm_kernel<1>), g, b, 0, s, X, R, W, O, S, cols, eps);
+  else if (cpt <= 2) IRON_LAUNCH((rmsnorm_kernel<2>), g, b, 0, s, X, R, W, O, S, cols, eps);
+  else if (cpt <= 4) IRON_LAUNCH((rmsnorm_kernel<4>), g, b, 0, s, X, R, W, O, S, cols, eps);
+  else IRON_LAUNCH((rmsnorm_kernel<8>), g, b, 0, s, X, R, W, O, S, cols, eps);
   return check_launch("rmsnorm");
 }
 
@@ -320,10 +320,10 @@ extern "C" int iron_softmax(const void* x, void* out, int rows, int cols, int va
   auto X = static_cast<const uint16_t*>(x);
   auto O = static_cast<uint16_t*>(out);
   dim3 g(rows), b(kBlock);
-  if (cpt <= 1) hipLaunchKernelGGL((softmax_kernel<1>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
-  else if (cpt <= 2) hipLaunchKernelGGL((softmax_kernel<2>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
-  else if (cpt <= 4) hipLaunchKernelGGL((softmax_kernel<4>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
-  else hipLaunchKernelGGL((softmax_kernel<8>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
+  if (cpt <= 1) IRON_LAUNCH((softmax_kernel<1>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
+  else if (cpt <= 2) IRON_LAUNCH((softmax_kernel<2>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
+  else if (cpt <= 4) IRON_LAUNCH((softmax_kernel<4>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
+  else IRON_LAUNCH((softmax_kernel<8>), g, b, 0, s, X, O, cols, valid_cols, valid_cols_dev);
   return check_launch("softmax");
 }
 
@@ -336,7 +336,7 @@ extern "C" int iron_rope(const void* x, const void* angles, int angles_fp32, voi
   IRON_REQUIRE(method == 0 || method == 1, "iron_rope: method_type must be 0 or 1, got %d", method);
   IRON_REQUIRE(out != x || method == 0 || method == 1, "iron_rope: bad aliasing");
   const long long pairs = static_cast<long long>(rows) * (cols / 2);
-  hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>((pairs + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+  IRON_LAUNCH(rope_kernel, dim3(static_cast<unsigned>((pairs + kBlock - 1) / kBlock)), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), angles, angles_fp32,
                      static_cast<uint16_t*>(out), rows, cols, angle_rows, method);
   return check_launch("rope");

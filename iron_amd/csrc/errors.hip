@@ -18,6 +18,7 @@ void set_error(const char* fmt, ...) {
 }
 
 int fail_einval(const char* fmt, ...) {
+  disarm_timing();
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
@@ -26,6 +27,7 @@ int fail_einval(const char* fmt, ...) {
 }
 
 int check_launch(const char* what) {
+  disarm_timing();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("%s: launch failed: %s", what, hipGetErrorString(e));
@@ -34,8 +36,31 @@ int check_launch(const char* what) {
   return 0;
 }
 
+static thread_local TimingEvents g_timing = {nullptr, nullptr};
+static thread_local bool g_timing_started = false;
+
+TimingEvents take_timing_events() {
+  TimingEvents t = g_timing;
+  if (t.stop && g_timing_started) t.start = nullptr;  // start stays on the first kernel
+  g_timing_started = g_timing.stop != nullptr;
+  return t;
+}
+
+void disarm_timing() {
+  g_timing = {nullptr, nullptr};
+  g_timing_started = false;
+}
+
 }  // namespace iron
 
 extern "C" const char* iron_last_error(void) { return iron::g_last_error; }
+
+extern "C" int iron_time_next_launch(void* start_event, void* stop_event) {
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return iron::fail_einval("iron_time_next_launch: give both events or neither");
+  iron::g_timing = {static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+  iron::g_timing_started = false;
+  return 0;
+}
 
 extern "C" int iron_abi_version(void) { return IRON_HIP_ABI_VERSION; }

@@ -191,7 +191,7 @@ extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, i
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi};
   const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt: problem too large");
-  hipLaunchKernelGGL(gemm_nt_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
+  IRON_LAUNCH(gemm_nt_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("gemm_bf16_nt");
 }
@@ -201,7 +201,7 @@ extern "C" int iron_transpose_bf16(const void* in, void* out, int rows, int cols
   IRON_REQUIRE(rows > 0 && cols > 0, "iron_transpose_bf16: empty matrix");
   dim3 grid((cols + 63) / 64, (rows + 63) / 64);
   IRON_REQUIRE(grid.y < 65536, "iron_transpose_bf16: too many rows");
-  hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+  IRON_LAUNCH(transpose_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(in), static_cast<uint16_t*>(out), rows, cols);
   return check_launch("transpose_bf16");
 }

@@ -23,13 +23,22 @@
 namespace iron {
 namespace {
 
+// norm_mode: what the optional RMSNorm does to the input vector x.
+//   NORM_NONE   : x used as given
+//   NORM_WEIGHT : x -> bf16(x * rsqrt(mean(x^2) + eps) * norm_w)  (reference order)
+//   NORM_SCALE  : outputs scaled by rsqrt(mean(x^2) + eps); the norm weight is
+//                 folded into the matrix columns beforehand, so no per-element
+//                 normalisation is needed (what the decode step uses)
+enum NormMode : int { NORM_NONE = 0, NORM_WEIGHT = 1, NORM_SCALE = 2 };
+
 struct GemvArgs {
   const uint16_t* W;       // (batches, M, K) bf16
   const uint16_t* W2;      // optional second (M, K) matrix (SwiGLU up projection)
   const uint16_t* x;       // (batches, K) bf16
   uint16_t* y;             // (batches, M) bf16
-  const uint16_t* norm_w;  // optional (K,) RMSNorm weight
+  const uint16_t* norm_w;  // (K,) RMSNorm weight for NORM_WEIGHT
   const uint16_t* resid;   // optional (M,) residual
+  unsigned long long* keys;  // optional argmax key per workgroup (4 rows)
   int M, K;
   float eps;
   int epi;
@@ -71,119 +80,162 @@ __device__ __forceinline__ float wave_inv_rms(const uint16_t* x, int K, float ep
   return rsqrtf(ss / static_cast<float>(K) + eps);
 }
 
-__device__ __forceinline__ void store_row(const GemvArgs& a, size_t idx, int row, float acc, float acc2,
-                                          bool pair) {
-  float v = pair ? silu_f32(acc) * acc2 : apply_epilogue(acc, a.epi);
-  if (a.resid) v += bf16_to_f32(a.resid[row]);
-  a.y[idx] = f32_to_bf16(v);
+// Final value of one output row (activation or SwiGLU, residual), stored as
+// bf16; returns the stored value for the argmax keys.
+__device__ __forceinline__ float finish_row(const uint16_t* resid, int epi, uint16_t* y, size_t idx, int row,
+                                            float acc, float acc2, bool pair) {
+  float v = pair ? silu_f32(acc) * acc2 : apply_epilogue(acc, epi);
+  if (resid) v += bf16_to_f32(resid[row]);
+  const uint16_t o = f32_to_bf16(v);
+  y[idx] = o;
+  return bf16_to_f32(o);
+}
+
+// Workgroup argmax of the rows its waves produced: keys[key_idx] = best key.
+// Every wave of the workgroup must call it (inactive waves pass key 0).
+__device__ __forceinline__ void publish_key(unsigned long long* keys, size_t key_idx, unsigned long long key) {
+  __shared__ unsigned long long ks[4];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & (kWave - 1)) == 0) ks[wave] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = ks[0];
+    for (int w = 1; w < 4; ++w) b = ks[w] > b ? ks[w] : b;
+    keys[key_idx] = b;
+  }
 }
 
 // Fast path: K == 512*U exactly; each lane holds U chunks of W (and W2) in
 // flight. One wave per output row.
-template <int U, bool PAIR, bool NORM>
+template <int U, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
-  if (row >= a.M) return;  // uniform per wave; the kernel has no block barrier
+  const bool active = row < a.M;  // uniform per wave
+  if (!active && !a.keys) return;  // without keys the kernel has no block barrier
+  unsigned long long key = 0;
+  if (active) {
+    const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
+    const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
+    const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff) + lane;
+    const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) + lane : nullptr;
+    const uint4* xv = reinterpret_cast<const uint4*>(x) + lane;
 
-  const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
-  const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
-  const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff) + lane;
-  const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) + lane : nullptr;
-  const uint4* xv = reinterpret_cast<const uint4*>(x) + lane;
-
-  uint4 w[U], w2[U], xc[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    w[u] = ld_stream16(Wr + u * kWave);
-    if (PAIR) w2[u] = ld_stream16(W2r + u * kWave);
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) xc[u] = xv[u * kWave];
-  if (NORM) {
-    float ss = 0.f;
-#pragma unroll
-    for (int u = 0; u < U; ++u) ss = sumsq_chunk(xc[u], ss);
-    const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
-    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w) + lane;
-#pragma unroll
-    for (int u = 0; u < U; ++u) xc[u] = normalize_chunk(xc[u], nw[u * kWave], inv);
-  }
-  float acc = 0.f, acc2 = 0.f;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    acc = dot_chunk(w[u], xc[u], acc);
-    if (PAIR) acc2 = dot_chunk(w2[u], xc[u], acc2);
-  }
-  acc = wave_sum(acc);
-  if (PAIR) acc2 = wave_sum(acc2);
-  if (lane == 0) store_row(a, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
-}
-
-// Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
-template <bool PAIR>
-__global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int b = blockIdx.y;
-  if (row >= a.M) return;
-  constexpr int U = 4;
-  const int nch = a.K >> 3;
-  const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
-  const float inv = a.norm_w ? wave_inv_rms(x, a.K, a.eps, lane) : 1.f;
-  const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
-  const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff);
-  const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) : nullptr;
-  float acc = 0.f, acc2 = 0.f;
-  for (int base = lane; base < nch; base += kWave * U) {
     uint4 w[U], w2[U], xc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int c = base + u * kWave;
-      const bool ok = c < nch;
-      w[u] = ok ? ld_stream16(Wr + c) : make_uint4(0, 0, 0, 0);
-      if (PAIR) w2[u] = ok ? ld_stream16(W2r + c) : make_uint4(0, 0, 0, 0);
-      xc[u] = ok ? xv[c] : make_uint4(0, 0, 0, 0);
-      if (ok && a.norm_w) xc[u] = normalize_chunk(xc[u], nw[c], inv);
+      w[u] = ld_stream16(Wr + u * kWave);
+      if (PAIR) w2[u] = ld_stream16(W2r + u * kWave);
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) xc[u] = xv[u * kWave];
+    float inv = 1.f;
+    if (NM != NORM_NONE) {
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) ss = sumsq_chunk(xc[u], ss);
+      inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+    }
+    if (NM == NORM_WEIGHT) {
+      const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w) + lane;
+#pragma unroll
+      for (int u = 0; u < U; ++u) xc[u] = normalize_chunk(xc[u], nw[u * kWave], inv);
+    }
+    float acc = 0.f, acc2 = 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       acc = dot_chunk(w[u], xc[u], acc);
       if (PAIR) acc2 = dot_chunk(w2[u], xc[u], acc2);
     }
+    acc = wave_sum(acc);
+    if (PAIR) acc2 = wave_sum(acc2);
+    if (NM == NORM_SCALE) {
+      acc *= inv;
+      acc2 *= inv;
+    }
+    float v = 0.f;
+    if (lane == 0) v = finish_row(a.resid, a.epi, a.y, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
+    if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
-  acc = wave_sum(acc);
-  if (PAIR) acc2 = wave_sum(acc2);
-  if (lane == 0) store_row(a, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
+  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + blockIdx.x, key);
+}
+
+// Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
+template <bool PAIR>
+__global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mode) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int b = blockIdx.y;
+  const bool active = row < a.M;
+  if (!active && !a.keys) return;
+  unsigned long long key = 0;
+  if (active) {
+    constexpr int U = 4;
+    const int nch = a.K >> 3;
+    const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
+    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+    const float inv = norm_mode != NORM_NONE ? wave_inv_rms(x, a.K, a.eps, lane) : 1.f;
+    const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
+    const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff);
+    const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) : nullptr;
+    float acc = 0.f, acc2 = 0.f;
+    for (int base = lane; base < nch; base += kWave * U) {
+      uint4 w[U], w2[U], xc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = base + u * kWave;
+        const bool ok = c < nch;
+        w[u] = ok ? ld_stream16(Wr + c) : make_uint4(0, 0, 0, 0);
+        if (PAIR) w2[u] = ok ? ld_stream16(W2r + c) : make_uint4(0, 0, 0, 0);
+        xc[u] = ok ? xv[c] : make_uint4(0, 0, 0, 0);
+        if (ok && norm_mode == NORM_WEIGHT) xc[u] = normalize_chunk(xc[u], nw[c], inv);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        acc = dot_chunk(w[u], xc[u], acc);
+        if (PAIR) acc2 = dot_chunk(w2[u], xc[u], acc2);
+      }
+    }
+    acc = wave_sum(acc);
+    if (PAIR) acc2 = wave_sum(acc2);
+    if (norm_mode == NORM_SCALE) {
+      acc *= inv;
+      acc2 *= inv;
+    }
+    float v = 0.f;
+    if (lane == 0) v = finish_row(a.resid, a.epi, a.y, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
+    if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
+  }
+  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + blockIdx.x, key);
 }
 
 template <int U, bool PAIR>
-void launch_bf16_fast(const GemvArgs& a, dim3 grid, hipStream_t s) {
-  if (a.norm_w)
-    hipLaunchKernelGGL((gemv_bf16_fast<U, PAIR, true>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((gemv_bf16_fast<U, PAIR, false>), grid, dim3(256), 0, s, a);
+void launch_bf16_fast(const GemvArgs& a, int norm_mode, dim3 grid, hipStream_t s) {
+  switch (norm_mode) {
+    case NORM_WEIGHT: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_WEIGHT>), grid, dim3(256), 0, s, a); break;
+    case NORM_SCALE: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_SCALE>), grid, dim3(256), 0, s, a); break;
+    default: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_NONE>), grid, dim3(256), 0, s, a); break;
+  }
 }
 
 template <bool PAIR>
-int launch_gemv_bf16(const GemvArgs& a, int batches, hipStream_t s) {
+int launch_gemv_bf16(const GemvArgs& a, int norm_mode, int batches, hipStream_t s) {
   dim3 grid((a.M + 3) / 4, batches);
   const int U = (a.K % 512 == 0) ? a.K / 512 : 0;
   switch (U) {
-    case 1: launch_bf16_fast<1, PAIR>(a, grid, s); break;
-    case 2: launch_bf16_fast<2, PAIR>(a, grid, s); break;
-    case 4: launch_bf16_fast<4, PAIR>(a, grid, s); break;
-    case 8: launch_bf16_fast<8, PAIR>(a, grid, s); break;
+    case 1: launch_bf16_fast<1, PAIR>(a, norm_mode, grid, s); break;
+    case 2: launch_bf16_fast<2, PAIR>(a, norm_mode, grid, s); break;
+    case 4: launch_bf16_fast<4, PAIR>(a, norm_mode, grid, s); break;
+    case 8: launch_bf16_fast<8, PAIR>(a, norm_mode, grid, s); break;
     case 16:
       if (!PAIR) {
-        launch_bf16_fast<16, false>(a, grid, s);
+        launch_bf16_fast<16, false>(a, norm_mode, grid, s);
         break;
       }
       [[fallthrough]];
-    default: hipLaunchKernelGGL((gemv_bf16_generic<PAIR>), grid, dim3(256), 0, s, a); break;
+    default: IRON_LAUNCH((gemv_bf16_generic<PAIR>), grid, dim3(256), 0, s, a, norm_mode); break;
   }
   return check_launch("gemv_bf16");
 }
@@ -209,6 +261,7 @@ struct I4Args {
   uint16_t* y;
   const uint16_t* norm_w;
   const uint16_t* resid;
+  unsigned long long* keys;  // optional argmax key per workgroup (4 rows; R forced to 1)
   int M, K;
   float eps;
   int epi;
@@ -260,140 +313,166 @@ __device__ __forceinline__ float i4_group_dot(uint4 c, const XGroup& g, uint32_t
   return acc;
 }
 
-__device__ __forceinline__ void store_i4_row(const I4Args& a, int row, float t, float t2, bool pair) {
-  float v = pair ? silu_f32(t) * t2 : apply_epilogue(t, a.epi);
-  if (a.resid) v += bf16_to_f32(a.resid[row]);
-  a.y[row] = f32_to_bf16(v);
-}
-
 // Fast path: K == 2048*GPL (every lane owns exactly GPL groups of a row) and
 // M % R == 0 (R rows per wave, sharing the x preparation).
-template <int GPL, int R, bool PAIR, bool NORM>
+template <int GPL, int R, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-  if (row0 >= a.M) return;  // uniform per wave
-  constexpr int G = GPL * kWave;
-  constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
+  const bool active = row0 < a.M;  // uniform per wave
+  if (!active && !a.keys) return;
+  unsigned long long key = 0;
+  if (active) {
+    constexpr int G = GPL * kWave;
+    constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
 
-  // Weight loads first, so they are in flight while x is prepared.
-  uint4 cw[R][GPL], cw2[R][GPL];
-  uint16_t sc[R][GPL], sc2[R][GPL];
+    // Weight loads first, so they are in flight while x is prepared.
+    uint4 cw[R][GPL], cw2[R][GPL];
+    uint16_t sc[R][GPL], sc2[R][GPL];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const size_t row = static_cast<size_t>(row0 + r);
+    for (int r = 0; r < R; ++r) {
+      const size_t row = static_cast<size_t>(row0 + r);
 #pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = lane + j * kWave;
-      cw[r][j] = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
-      sc[r][j] = a.scales[row * G + g];
-      if (PAIR) {
-        cw2[r][j] = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
-        sc2[r][j] = a.scales2[row * G + g];
+      for (int j = 0; j < GPL; ++j) {
+        const int g = lane + j * kWave;
+        cw[r][j] = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
+        sc[r][j] = a.scales[row * G + g];
+        if (PAIR) {
+          cw2[r][j] = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
+          sc2[r][j] = a.scales2[row * G + g];
+        }
       }
     }
-  }
 
-  uint4 xr[GPL][4];
-  const uint4* xv = reinterpret_cast<const uint4*>(a.x);
-#pragma unroll
-  for (int j = 0; j < GPL; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) xr[j][q] = xv[(lane + j * kWave) * 4 + q];
-  if (NORM) {
-    float ss = 0.f;
+    uint4 xr[GPL][4];
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x);
 #pragma unroll
     for (int j = 0; j < GPL; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[j][q], ss);
-    const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
-    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+      for (int q = 0; q < 4; ++q) xr[j][q] = xv[(lane + j * kWave) * 4 + q];
+    float inv = 1.f;
+    if (NM != NORM_NONE) {
+      float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < GPL; ++j)
+      for (int j = 0; j < GPL; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xr[j][q] = normalize_chunk(xr[j][q], nw[(lane + j * kWave) * 4 + q], inv);
-  }
-  XGroup xg[GPL];
+        for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[j][q], ss);
+      inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+    }
+    if (NM == NORM_WEIGHT) {
+      const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
 #pragma unroll
-  for (int j = 0; j < GPL; ++j) build_xgroup(xr[j], xg[j]);
+      for (int j = 0; j < GPL; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xr[j][q] = normalize_chunk(xr[j][q], nw[(lane + j * kWave) * 4 + q], inv);
+    }
+    XGroup xg[GPL];
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) build_xgroup(xr[j], xg[j]);
 
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float acc = 0.f, acc2 = 0.f;
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.f, acc2 = 0.f;
 #pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const float d = i4_group_dot(cw[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
-      acc = fmaf(bf16_to_f32(sc[r][j]), d, acc);
-      if (PAIR) {
-        const float d2 = i4_group_dot(cw2[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
-        acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
+      for (int j = 0; j < GPL; ++j) {
+        const float d = i4_group_dot(cw[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+        acc = fmaf(bf16_to_f32(sc[r][j]), d, acc);
+        if (PAIR) {
+          const float d2 = i4_group_dot(cw2[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+          acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
+        }
+      }
+      float t = wave_sum(acc);
+      float t2 = PAIR ? wave_sum(acc2) : 0.f;
+      if (NM == NORM_SCALE) {
+        t *= inv;
+        t2 *= inv;
+      }
+      float v = 0.f;
+      if (lane == 0) v = finish_row(a.resid, a.epi, a.y, row0 + r, row0 + r, t, t2, PAIR);
+      if (a.keys) {
+        const unsigned long long k = argmax_key(__shfl(v, 0, kWave), row0 + r);
+        key = k > key ? k : key;
       }
     }
-    const float t = wave_sum(acc);
-    const float t2 = PAIR ? wave_sum(acc2) : 0.f;
-    if (lane == 0) store_i4_row(a, row0 + r, t, t2, PAIR);
   }
+  if (a.keys) publish_key(a.keys, blockIdx.x, key);
 }
 
 // Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
 template <bool PAIR>
-__global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a) {
+__global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) {
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= a.M) return;
-  const int G = a.K >> 5;
-  const size_t crow = static_cast<size_t>(a.K) >> 1;
-  const uint4* xv = reinterpret_cast<const uint4*>(a.x);
-  const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
-  const float inv = a.norm_w ? wave_inv_rms(a.x, a.K, a.eps, lane) : 1.f;
-  float acc = 0.f, acc2 = 0.f;
-  for (int g = lane; g < G; g += kWave) {
-    const uint4 c = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
-    const float s = bf16_to_f32(a.scales[static_cast<size_t>(row) * G + g]);
-    uint4 c2 = make_uint4(0, 0, 0, 0);
-    float s2 = 0.f;
-    if (PAIR) {
-      c2 = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
-      s2 = bf16_to_f32(a.scales2[static_cast<size_t>(row) * G + g]);
-    }
-    uint4 xc[4];
+  const bool active = row < a.M;
+  if (!active && !a.keys) return;
+  unsigned long long key = 0;
+  if (active) {
+    const int G = a.K >> 5;
+    const size_t crow = static_cast<size_t>(a.K) >> 1;
+    const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+    const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
+    const float inv = norm_mode != NORM_NONE ? wave_inv_rms(a.x, a.K, a.eps, lane) : 1.f;
+    float acc = 0.f, acc2 = 0.f;
+    for (int g = lane; g < G; g += kWave) {
+      const uint4 c = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
+      const float s = bf16_to_f32(a.scales[static_cast<size_t>(row) * G + g]);
+      uint4 c2 = make_uint4(0, 0, 0, 0);
+      float s2 = 0.f;
+      if (PAIR) {
+        c2 = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
+        s2 = bf16_to_f32(a.scales2[static_cast<size_t>(row) * G + g]);
+      }
+      uint4 xc[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      xc[q] = xv[g * 4 + q];
-      if (a.norm_w) xc[q] = normalize_chunk(xc[q], nw[g * 4 + q], inv);
+      for (int q = 0; q < 4; ++q) {
+        xc[q] = xv[g * 4 + q];
+        if (norm_mode == NORM_WEIGHT) xc[q] = normalize_chunk(xc[q], nw[g * 4 + q], inv);
+      }
+      XGroup t;
+      build_xgroup(xc, t);
+      acc = fmaf(s, i4_group_dot(c, t, a.magic) - a.offset * t.sum, acc);
+      if (PAIR) acc2 = fmaf(s2, i4_group_dot(c2, t, a.magic) - a.offset * t.sum, acc2);
     }
-    XGroup t;
-    build_xgroup(xc, t);
-    acc = fmaf(s, i4_group_dot(c, t, a.magic) - a.offset * t.sum, acc);
-    if (PAIR) acc2 = fmaf(s2, i4_group_dot(c2, t, a.magic) - a.offset * t.sum, acc2);
+    float t = wave_sum(acc);
+    float t2 = PAIR ? wave_sum(acc2) : 0.f;
+    if (norm_mode == NORM_SCALE) {
+      t *= inv;
+      t2 *= inv;
+    }
+    float v = 0.f;
+    if (lane == 0) v = finish_row(a.resid, a.epi, a.y, row, row, t, t2, PAIR);
+    if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
-  const float t = wave_sum(acc);
-  const float t2 = PAIR ? wave_sum(acc2) : 0.f;
-  if (lane == 0) store_i4_row(a, row, t, t2, PAIR);
+  if (a.keys) publish_key(a.keys, blockIdx.x, key);
 }
 
 template <int GPL, int R, bool PAIR>
-void launch_i4_fast(const I4Args& a, hipStream_t s) {
+void launch_i4_fast(const I4Args& a, int norm_mode, hipStream_t s) {
   dim3 grid((a.M / R + 3) / 4), block(256);
-  if (a.norm_w)
-    hipLaunchKernelGGL((gemv_i4_fast<GPL, R, PAIR, true>), grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL((gemv_i4_fast<GPL, R, PAIR, false>), grid, block, 0, s, a);
+  switch (norm_mode) {
+    case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_WEIGHT>), grid, block, 0, s, a); break;
+    case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_SCALE>), grid, block, 0, s, a); break;
+    default: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_NONE>), grid, block, 0, s, a); break;
+  }
 }
 
 template <bool PAIR>
-int launch_gemv_i4(const I4Args& a, hipStream_t s) {
+int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
   const int gpl = (a.K % 2048 == 0) ? a.K / 2048 : 0;
-  // Two rows per wave when there are enough rows to keep >= 4 waves per SIMD.
-  const bool r2 = !PAIR && a.M % 2 == 0 && a.M >= 8192;
+  // Two rows per wave when there are enough rows to keep >= 4 waves per SIMD
+  // (not with argmax keys, which are defined per 4 rows).
+  const bool r2 = !PAIR && !a.keys && a.M % 2 == 0 && a.M >= 8192;
   switch (gpl) {
     case 1:
-      if (r2) launch_i4_fast<1, 2, PAIR>(a, s);
-      else launch_i4_fast<1, 1, PAIR>(a, s);
+      if (r2) launch_i4_fast<1, 2, PAIR>(a, norm_mode, s);
+      else launch_i4_fast<1, 1, PAIR>(a, norm_mode, s);
       break;
-    case 2: launch_i4_fast<2, 1, PAIR>(a, s); break;
-    case 4: launch_i4_fast<4, 1, PAIR>(a, s); break;
-    default: hipLaunchKernelGGL((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a); break;
+    case 2: launch_i4_fast<2, 1, PAIR>(a, norm_mode, s); break;
+    case 4: launch_i4_fast<4, 1, PAIR>(a, norm_mode, s); break;
+    default:
+      IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
+      break;
   }
   return check_launch("gemv_i4g32");
 }
@@ -469,41 +548,55 @@ extern "C" int iron_gemv_bf16(const void* W, const void* x, void* y, int M, int 
   IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16: bad epilogue %d",
                epilogue);
   GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x),
-             static_cast<uint16_t*>(y), nullptr, nullptr, M, K, 0.f, epilogue};
-  return launch_gemv_bf16<false>(a, batches, static_cast<hipStream_t>(stream));
+             static_cast<uint16_t*>(y), nullptr, nullptr, nullptr, M, K, 0.f, epilogue};
+  return launch_gemv_bf16<false>(a, NORM_NONE, batches, static_cast<hipStream_t>(stream));
+}
+
+static int check_norm(const char* fn, int norm_mode, const void* norm_w) {
+  IRON_REQUIRE(norm_mode >= NORM_NONE && norm_mode <= NORM_SCALE, "%s: bad norm_mode %d", fn, norm_mode);
+  IRON_REQUIRE((norm_mode == NORM_WEIGHT) == (norm_w != nullptr), "%s: norm_w is required for norm_mode 1 only", fn);
+  return 0;
 }
 
 extern "C" int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x, void* y, int M, int K,
-                                    const void* norm_w, float eps, const void* residual, int epilogue,
-                                    void* stream) {
+                                    int norm_mode, const void* norm_w, float eps, const void* residual, int epilogue,
+                                    void* argmax_keys, void* stream) {
   IRON_REQUIRE(W && x && y, "iron_gemv_bf16_fused: null pointer");
   IRON_REQUIRE(M > 0 && K > 0 && K % 8 == 0, "iron_gemv_bf16_fused: M=%d K=%d (K must be a multiple of 8)",
                M, K);
   IRON_REQUIRE(aligned16(W) && aligned16(x) && (!W2 || aligned16(W2)) && (!norm_w || aligned16(norm_w)),
                "iron_gemv_bf16_fused: operands must be 16-byte aligned");
+  if (int rc = check_norm("iron_gemv_bf16_fused", norm_mode, norm_w)) return rc;
   IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16_fused: bad epilogue %d",
                epilogue);
   IRON_REQUIRE(!(W2 && epilogue != EPI_NONE), "iron_gemv_bf16_fused: the SwiGLU pair takes no epilogue");
   IRON_REQUIRE(y != x, "iron_gemv_bf16_fused: y must not alias x");
-  GemvArgs a{static_cast<const uint16_t*>(W),      static_cast<const uint16_t*>(W2),
-             static_cast<const uint16_t*>(x),      static_cast<uint16_t*>(y),
-             static_cast<const uint16_t*>(norm_w), static_cast<const uint16_t*>(residual),
-             M,                                    K,
-             eps,                                  epilogue};
+  IRON_REQUIRE((reinterpret_cast<uintptr_t>(argmax_keys) & 7u) == 0, "iron_gemv_bf16_fused: keys must be 8-byte aligned");
+  GemvArgs a{static_cast<const uint16_t*>(W),
+             static_cast<const uint16_t*>(W2),
+             static_cast<const uint16_t*>(x),
+             static_cast<uint16_t*>(y),
+             static_cast<const uint16_t*>(norm_w),
+             static_cast<const uint16_t*>(residual),
+             static_cast<unsigned long long*>(argmax_keys),
+             M,
+             K,
+             eps,
+             epilogue};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return W2 ? launch_gemv_bf16<true>(a, 1, s) : launch_gemv_bf16<false>(a, 1, s);
+  return W2 ? launch_gemv_bf16<true>(a, norm_mode, 1, s) : launch_gemv_bf16<false>(a, norm_mode, 1, s);
 }
 
 extern "C" int iron_gemv_i4g32(const void* codes, const void* scales, const void* x, void* y, int M, int K,
                                int is_signed, void* stream) {
-  return iron_gemv_i4g32_fused(codes, scales, nullptr, nullptr, x, y, M, K, is_signed, nullptr, 0.f, nullptr,
-                               0, stream);
+  return iron_gemv_i4g32_fused(codes, scales, nullptr, nullptr, x, y, M, K, is_signed, NORM_NONE, nullptr, 0.f,
+                               nullptr, 0, nullptr, stream);
 }
 
 extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, const void* codes2,
                                      const void* scales2, const void* x, void* y, int M, int K, int is_signed,
-                                     const void* norm_w, float eps, const void* residual, int epilogue,
-                                     void* stream) {
+                                     int norm_mode, const void* norm_w, float eps, const void* residual, int epilogue,
+                                     void* argmax_keys, void* stream) {
   IRON_REQUIRE(codes && scales && x && y, "iron_gemv_i4g32: null pointer");
   IRON_REQUIRE((codes2 == nullptr) == (scales2 == nullptr), "iron_gemv_i4g32: codes2/scales2 come together");
   IRON_REQUIRE(M > 0 && K > 0 && K % 32 == 0, "iron_gemv_i4g32: M=%d K=%d (K must be a multiple of 32)", M,
@@ -512,10 +605,12 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
                    (!norm_w || aligned16(norm_w)),
                "iron_gemv_i4g32: codes, x and norm weight must be 16-byte aligned");
   IRON_REQUIRE((reinterpret_cast<uintptr_t>(scales) & 1u) == 0, "iron_gemv_i4g32: scales must be 2-byte aligned");
+  if (int rc = check_norm("iron_gemv_i4g32", norm_mode, norm_w)) return rc;
   IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_i4g32: bad epilogue %d",
                epilogue);
   IRON_REQUIRE(!(codes2 && epilogue != EPI_NONE), "iron_gemv_i4g32: the SwiGLU pair takes no epilogue");
   IRON_REQUIRE(y != x, "iron_gemv_i4g32: y must not alias x");
+  IRON_REQUIRE((reinterpret_cast<uintptr_t>(argmax_keys) & 7u) == 0, "iron_gemv_i4g32: keys must be 8-byte aligned");
   I4Args a{static_cast<const uint8_t*>(codes),
            static_cast<const uint16_t*>(scales),
            static_cast<const uint8_t*>(codes2),
@@ -524,6 +619,7 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
            static_cast<uint16_t*>(y),
            static_cast<const uint16_t*>(norm_w),
            static_cast<const uint16_t*>(residual),
+           static_cast<unsigned long long*>(argmax_keys),
            M,
            K,
            eps,
@@ -531,7 +627,7 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
            is_signed ? 0x43084308u : 0x43004300u,
            is_signed ? 136.f : 128.f};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return codes2 ? launch_gemv_i4<true>(a, s) : launch_gemv_i4<false>(a, s);
+  return codes2 ? launch_gemv_i4<true>(a, norm_mode, s) : launch_gemv_i4<false>(a, norm_mode, s);
 }
 
 extern "C" int iron_dequant_i4(const void* codes, const void* scales, void* out, int N, int K, int group,
@@ -543,7 +639,7 @@ extern "C" int iron_dequant_i4(const void* codes, const void* scales, void* out,
   IRON_REQUIRE(aligned16(out) && (reinterpret_cast<uintptr_t>(codes) & 3u) == 0,
                "iron_dequant_i4: out must be 16-byte and codes 4-byte aligned");
   const size_t threads = static_cast<size_t>(N) * (K / 8);
-  hipLaunchKernelGGL(dequant_planar_kernel, dim3((threads + 255) / 256), dim3(256), 0,
+  IRON_LAUNCH(dequant_planar_kernel, dim3((threads + 255) / 256), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(codes),
                      static_cast<const uint16_t*>(scales), static_cast<uint16_t*>(out), N, K, group, is_signed);
   return check_launch("dequant_i4");
@@ -559,7 +655,7 @@ extern "C" int iron_dequant_i4_payload(const void* payload, void* out, long long
                "iron_dequant_i4_payload: group_size %d must be even and divide tile_size %d", group_size,
                tile_size);
   const long long threads = size / 2;
-  hipLaunchKernelGGL(dequant_payload_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+  IRON_LAUNCH(dequant_payload_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(payload),
                      static_cast<uint16_t*>(out), size, tile_size, group_size, is_signed);
   return check_launch("dequant_i4_payload");
@@ -613,7 +709,7 @@ extern "C" int iron_quantize_i4g32(const void* W, void* codes, void* scales, int
   IRON_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "iron_quantize_i4g32: N=%d K=%d (K must be a multiple of 32)", N, K);
   IRON_REQUIRE(aligned16(W) && aligned16(codes), "iron_quantize_i4g32: W and codes must be 16-byte aligned");
   const long long groups = static_cast<long long>(N) * (K / 32);
-  hipLaunchKernelGGL(quantize_i4g32_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
+  IRON_LAUNCH(quantize_i4g32_kernel, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(W), static_cast<uint8_t*>(codes),
                      static_cast<uint16_t*>(scales), groups);
   return check_launch("quantize_i4g32");

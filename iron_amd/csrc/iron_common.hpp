@@ -6,6 +6,7 @@
 // what makes the int4 dequant bit-exact against the test oracle).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -19,20 +20,33 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even narrowing; NaN stays a (quiet) NaN.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even narrowing of two floats in one v_cvt_pk_bf16_f32
+// (NaN stays a quiet NaN); `lo` lands in bits 0..15.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>(cvt_pk_bf16(f, 0.f) & 0xffffu);
 }
 
 // Low / high bf16 of a packed 32-bit word, widened to fp32.
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
+
+// Argmax key: unsigned order of (value, -index), so the largest key is the
+// largest value and, among equal values, the smallest index.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<unsigned long long>(ord) << 32) | (0xffffffffu - idx);
+}
+__device__ __forceinline__ uint32_t argmax_key_index(unsigned long long k) {
+  return 0xffffffffu - static_cast<uint32_t>(k & 0xffffffffu);
 }
 
 // acc + a.lo*b.lo + a.hi*b.hi with fp32 accumulation (v_dot2c_f32_bf16).
@@ -130,7 +144,28 @@ void set_error(const char* fmt, ...);
 int fail_einval(const char* fmt, ...);
 int check_launch(const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Events armed by iron_time_next_launch() for this thread's next entry-point
+// call: `start` is recorded at the start of its first kernel, `stop` at the
+// end of every kernel it launches (so at the end of the last one).
+struct TimingEvents {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+TimingEvents take_timing_events();  // events for this launch (start only on the first)
+void disarm_timing();               // end of an entry point (called by check_launch)
 }  // namespace iron
+
+// Every kernel launch goes through here: with timing events armed, the launch
+// records them at the kernel's own start and end (hipExtLaunchKernelGGL).
+#define IRON_LAUNCH(kernel, grid, block, shmem, stream, ...)                                          \
+  do {                                                                                                \
+    const ::iron::TimingEvents _te = ::iron::take_timing_events();                                  \
+    if (_te.stop)                                                                                     \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, _te.start, _te.stop, 0, __VA_ARGS__); \
+    else                                                                                              \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                            \
+  } while (0)
 
 #define IRON_EINVAL 22
 #define IRON_REQUIRE(cond, ...)                         \

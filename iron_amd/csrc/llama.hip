@@ -72,6 +72,47 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict
   }
 }
 
+// Greedy token selection from the per-workgroup argmax keys of the LM-head
+// GEMV, fused with the bookkeeping and the next token's embedding (one
+// 1024-thread workgroup): token_out = argmax; history[*pos] = token;
+// *pos += 1; x_out = table[token] (skipped when table is NULL).
+__global__ __launch_bounds__(1024) void select_embed_kernel(const unsigned long long* __restrict__ keys, int n_keys,
+                                                            const uint16_t* __restrict__ table, int dim, int vocab,
+                                                            uint16_t* __restrict__ x_out, int* token_out, int* pos,
+                                                            int* history, int history_cap) {
+  __shared__ unsigned long long ks[16];
+  __shared__ int tok_s;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < n_keys; i += 1024) {
+    const unsigned long long k = keys[i];
+    best = k > best ? k : best;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const unsigned long long o = __shfl_xor(best, off, kWave);
+    best = o > best ? o : best;
+  }
+  if ((threadIdx.x & 63) == 0) ks[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = ks[0];
+    for (int w = 1; w < 16; ++w) b = ks[w] > b ? ks[w] : b;
+    int tok = static_cast<int>(argmax_key_index(b));
+    if (tok < 0 || tok >= vocab) tok = 0;
+    tok_s = tok;
+    token_out[0] = tok;
+    if (pos) {
+      const int p = *pos;
+      if (history && p >= 0 && p < history_cap) history[p] = tok;
+      *pos = p + 1;
+    }
+  }
+  __syncthreads();
+  if (table) {
+    const uint4* src = reinterpret_cast<const uint4*>(table + static_cast<size_t>(tok_s) * dim);
+    for (int c = threadIdx.x; c < (dim >> 3); c += 1024) reinterpret_cast<uint4*>(x_out)[c] = src[c];
+  }
+}
+
 // Prefill: qkv (S, (H + 2*Hkv) * 64) rows -> q_out (S, H*64) rotated,
 // k_cache[:, pos0+s] rotated, v_cache[:, pos0+s] copied. One thread per
 // rotated pair (q and k heads) or per v element pair.
@@ -113,7 +154,7 @@ extern "C" int iron_embedding(const void* table, const int* ids, void* out, int 
   IRON_REQUIRE(n > 0 && dim > 0 && dim % 8 == 0 && vocab > 0, "iron_embedding: n=%d dim=%d vocab=%d", n, dim, vocab);
   IRON_REQUIRE(aligned16(table) && aligned16(out), "iron_embedding: table and out must be 16-byte aligned");
   const long long threads = static_cast<long long>(n) * (dim / 8);
-  hipLaunchKernelGGL(embedding_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+  IRON_LAUNCH(embedding_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(table), ids,
                      static_cast<uint16_t*>(out), n, dim, vocab);
   return check_launch("embedding");
@@ -124,9 +165,22 @@ extern "C" int iron_argmax_bf16(const void* x, int n, int* token_out, int* pos, 
   IRON_REQUIRE(x && token_out, "iron_argmax_bf16: null pointer");
   IRON_REQUIRE(n > 0, "iron_argmax_bf16: empty input");
   IRON_REQUIRE(!history || pos, "iron_argmax_bf16: history needs a position counter");
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+  IRON_LAUNCH(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(x), n, token_out, pos, history, history_cap);
   return check_launch("argmax");
+}
+
+extern "C" int iron_argmax_select(const void* keys, int n_keys, const void* table, int dim, int vocab, void* x_out,
+                                  int* token_out, int* pos, int* history, int history_cap, void* stream) {
+  IRON_REQUIRE(keys && token_out && n_keys > 0, "iron_argmax_select: null pointer or no keys");
+  IRON_REQUIRE(vocab > 0, "iron_argmax_select: vocab must be positive");
+  IRON_REQUIRE(!table || (x_out && dim > 0 && dim % 8 == 0 && aligned16(table) && aligned16(x_out)),
+               "iron_argmax_select: embedding needs x_out, dim %% 8 == 0 and 16-byte alignment");
+  IRON_REQUIRE(!history || pos, "iron_argmax_select: history needs a position counter");
+  IRON_LAUNCH(select_embed_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+              static_cast<const unsigned long long*>(keys), n_keys, static_cast<const uint16_t*>(table), dim, vocab,
+              static_cast<uint16_t*>(x_out), token_out, pos, history, history_cap);
+  return check_launch("argmax_select");
 }
 
 extern "C" int iron_qkv_rope_scatter(const void* qkv, const float* angles, int angle_rows, void* q_out, void* k_cache,
@@ -139,7 +193,7 @@ extern "C" int iron_qkv_rope_scatter(const void* qkv, const float* angles, int a
                "iron_qkv_rope_scatter: positions [%d, %d) exceed the cache (%d) or angle table (%d)", pos0,
                pos0 + seq, max_len, angle_rows);
   const long long threads = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
-  hipLaunchKernelGGL(qkv_scatter_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+  IRON_LAUNCH(qkv_scatter_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), angles,
                      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
                      seq, n_heads, n_kv_heads, max_len, pos0);

@@ -111,7 +111,8 @@ class LlamaCPU:
             x = x + swiglu_ffn_forward(h, w[p + "mlp.gate_proj.weight"], w[p + "mlp.up_proj.weight"],
                                        w[p + "mlp.down_proj.weight"])
         x = rms_norm_forward(x, w["model.norm.weight"])
-        return torch.nn.functional.linear(x, w["model.embed_tokens.weight"])
+        head = w.get("lm_head.weight", w["model.embed_tokens.weight"])  # tied unless given (HF convention)
+        return torch.nn.functional.linear(x, head)
 
 
 def kl_and_top1(ref_logits: torch.Tensor, cand_logits: torch.Tensor):

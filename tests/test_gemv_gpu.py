@@ -157,3 +157,108 @@ def test_dequant_payload_bit_exact(gpu, n, cols, ch, tile):
     op.get_callable()(payload.to(gpu), out)
     torch.cuda.synchronize()
     assert _bits_equal(out, ref)
+
+
+def _i4(W, gpu):
+    from iron_amd import _lib
+
+    Wd = W.to(gpu)
+    c = torch.empty(W.shape[0], W.shape[1] // 2, dtype=torch.uint8, device=gpu)
+    s = torch.empty(W.shape[0], W.shape[1] // 32, dtype=BF16, device=gpu)
+    _lib.call("iron_quantize_i4g32", Wd.data_ptr(), c.data_ptr(), s.data_ptr(), W.shape[0], W.shape[1],
+              _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    return c, s
+
+
+def test_quantizer_matches_oracle_bit_exact(gpu):
+    W = (torch.randn(512, 2048, generator=torch.Generator().manual_seed(3)) * 0.02).to(BF16)
+    c, s = _i4(W, gpu)
+    rc, rs = ops.quantize_int4_g32(W)
+    assert torch.equal(c.cpu(), rc) and _bits_equal(s, rs)
+
+
+@pytest.mark.parametrize("int4", [False, True])
+@pytest.mark.parametrize("mode", [1, 2])
+def test_config4_swiglu_block(gpu, int4, mode):
+    """x + Wd(silu(Wg xn) * (Wu xn)), xn = RMSNorm(x) * w, two
+    fused GEMV launches. mode 1 normalises x (reference order); mode 2 folds the
+    norm weight into Wg/Wu and scales the outputs. Bar: max-abs 2e-2, rel-L2 1e-2
+    against the fp32 chain on the same (dequantised) weights."""
+    from iron_amd import _lib
+
+    x, nw, Wg, Wu, Wd = configs.cfg4_swiglu_block()
+    E, F = 2048, 8192
+    if mode == 2:
+        Wg_run = (Wg.float() * nw.float()).to(BF16)
+        Wu_run = (Wu.float() * nw.float()).to(BF16)
+    else:
+        Wg_run, Wu_run = Wg, Wu
+    s = _lib.stream_handle(gpu)
+    xd, nwd = x.to(gpu), nw.to(gpu)
+    h = torch.empty(F, dtype=BF16, device=gpu)
+    y = torch.empty(E, dtype=BF16, device=gpu)
+    if int4:
+        (gc, gs), (uc, us), (dc, ds) = _i4(Wg_run, gpu), _i4(Wu_run, gpu), _i4(Wd, gpu)
+        _lib.call("iron_gemv_i4g32_fused", gc.data_ptr(), gs.data_ptr(), uc.data_ptr(), us.data_ptr(), xd.data_ptr(),
+                  h.data_ptr(), F, E, 1, mode, nwd.data_ptr() if mode == 1 else None, 1e-5, None, 0, None, s)
+        _lib.call("iron_gemv_i4g32_fused", dc.data_ptr(), ds.data_ptr(), None, None, h.data_ptr(), y.data_ptr(), E, F,
+                  1, 0, None, 0.0, xd.data_ptr(), 0, None, s)
+        Wg_eff = ops.dequant_planar(gc.cpu(), gs.cpu()).float()
+        Wu_eff = ops.dequant_planar(uc.cpu(), us.cpu()).float()
+        Wd_eff = ops.dequant_planar(dc.cpu(), ds.cpu()).float()
+    else:
+        Gd, Ud, Dd = Wg_run.to(gpu), Wu_run.to(gpu), Wd.to(gpu)
+        _lib.call("iron_gemv_bf16_fused", Gd.data_ptr(), Ud.data_ptr(), xd.data_ptr(), h.data_ptr(), F, E, mode,
+                  nwd.data_ptr() if mode == 1 else None, 1e-5, None, 0, None, s)
+        _lib.call("iron_gemv_bf16_fused", Dd.data_ptr(), None, h.data_ptr(), y.data_ptr(), E, F, 0, None, 0.0,
+                  xd.data_ptr(), 0, None, s)
+        Wg_eff, Wu_eff, Wd_eff = Wg_run.float(), Wu_run.float(), Wd.float()
+    torch.cuda.synchronize()
+    xf = x.float()
+    xhat = xf / torch.sqrt((xf * xf).mean() + 1e-5)
+    xn = xhat * nw.float() if mode == 1 else xhat
+    hr = torch.nn.functional.silu(Wg_eff @ xn) * (Wu_eff @ xn)
+    ref = xf + Wd_eff @ hr
+    max_abs, rel_l2 = ops.max_abs_rel_l2(y, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+    if not int4:  # against the reference operator chain (bf16 between steps, same weights)
+        chain = ops.swiglu_block_reference(x, nw, Wg, Wu, Wd)
+        assert ops.max_abs_rel_l2(y, chain)[1] <= 2e-2
+
+
+@pytest.mark.parametrize("int4", [False, True])
+@pytest.mark.parametrize("M", [1000, 128256])
+def test_argmax_keys_and_select(gpu, int4, M):
+    """GEMV argmax keys + iron_argmax_select == torch.argmax of the GEMV's own
+    bf16 output (first index on ties); the selected row is embedded."""
+    from iron_amd import _lib
+
+    K = 2048
+    g = torch.Generator().manual_seed(M)
+    W = (torch.randn(M, K, generator=g) * 0.02).to(BF16)
+    x = torch.randn(K, generator=g).to(BF16)
+    s = _lib.stream_handle(gpu)
+    xd = x.to(gpu)
+    y = torch.empty(M, dtype=BF16, device=gpu)
+    nk = (M + 3) // 4
+    keys = torch.zeros(nk, dtype=torch.int64, device=gpu)
+    if int4:
+        c, sc = _i4(W, gpu)
+        _lib.call("iron_gemv_i4g32_fused", c.data_ptr(), sc.data_ptr(), None, None, xd.data_ptr(), y.data_ptr(), M, K,
+                  1, 2, None, 1e-5, None, 0, keys.data_ptr(), s)
+    else:
+        Wd = W.to(gpu)
+        _lib.call("iron_gemv_bf16_fused", Wd.data_ptr(), None, xd.data_ptr(), y.data_ptr(), M, K, 2, None, 1e-5, None,
+                  0, keys.data_ptr(), s)
+    table = torch.randn(M, 64, generator=g).to(BF16).to(gpu)
+    xo = torch.empty(64, dtype=BF16, device=gpu)
+    tok = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pos = torch.tensor([5], dtype=torch.int32, device=gpu)
+    hist = torch.full((8,), -1, dtype=torch.int32, device=gpu)
+    _lib.call("iron_argmax_select", keys.data_ptr(), nk, table.data_ptr(), 64, M, xo.data_ptr(), tok.data_ptr(),
+              pos.data_ptr(), hist.data_ptr(), 8, s)
+    torch.cuda.synchronize()
+    expect = int(torch.argmax(y.cpu().float()))
+    assert int(tok.item()) == expect and int(hist[5].item()) == expect and int(pos.item()) == 6
+    assert torch.equal(xo.cpu(), table[expect].cpu())
