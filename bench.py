@@ -1,7 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-model]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--mode full|gemv|model]
+
+--mode gemv runs only the headline kernel (plus three 64 MiB device copies
+that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
+runs only the Llama configuration. Both print the same JSON line shape.
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
@@ -38,6 +42,11 @@ BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 POOL_BYTES = 640 << 20  # rotate through > 512 MiB of distinct weights
 
 METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
+
+# HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE +
+# WRITE_SIZE, each scaled by the counter's reading for a copy of known size
+# (profiles/gemv_i4g32_cfg2_pmc.md).
+TRAFFIC_BYTES = 9567678
 
 
 class HipEvents:
@@ -379,8 +388,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-model", action="store_true")
-    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--mode", choices=["full", "gemv", "model"], default="full")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -401,6 +409,11 @@ def main() -> int:
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     tm = Timer(torch, lib)
+
+    if args.mode == "model":
+        out = {"metric": METRIC, "mode": "model", "extra": {"llama_cfg5": bench_model(torch, dev)}}
+        print(json.dumps(out), flush=True)
+        return 0
 
     i4 = bench_gemv_int4(torch, lib, tm, dev, args.steps, args.warmup)
     value = i4["bytes"] * args.steps / (i4["wall_ms"] * 1e-3) / 1e9
@@ -430,23 +443,29 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "gemv_i4_fast<1, 2, false, false>",
+            "traffic": TRAFFIC_BYTES,
+            "kernel": "gemv_i4_fast<1, 2, false, 0>",
             "kernel_us": round(i4["kernel_us"], 3),
         },
     }
-    if not args.no_extra:
+    if args.mode == "gemv":
+        # calibration for the PMC runs: 64 MiB device-to-device copies (known bytes)
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    else:
         extra = {
             "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300),
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
             "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200),
             "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+            "llama_cfg5": bench_model(torch, dev),
         }
-        if not args.no_model:
-            extra["llama_cfg5"] = bench_model(torch, dev)
         out["extra"] = extra
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_int4(torch, i4["inputs"], args.cpu_seconds)
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_int4(torch, i4["inputs"], args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
 
