@@ -146,3 +146,23 @@ def test_gemv_int4_reference_is_composition():
     bound = exact.abs() * 2**-8 + (q.abs() * scales.double().repeat_interleave(32, 1)).matmul(x.double().abs()) * 2**-8
     assert torch.all(err <= bound + 1e-6)
     assert W.dtype == BF16
+
+
+def test_quantizer_picks_nearest_code_and_bf16_scale():
+    """quantize_int4_g32 against a float64 brute force over all 16 codes."""
+    torch.manual_seed(5)
+    W = (torch.randn(16, 256) * 0.02).to(BF16)
+    W[0, :32] = 0  # an all-zero group
+    codes, scales = ops.quantize_int4_g32(W)
+    Wd = W.double().reshape(16, 8, 32)
+    amax = Wd.abs().amax(-1)
+    assert torch.equal(scales, (amax.clamp_min(1e-8) / 7).float().to(BF16))
+    s = scales.double().unsqueeze(-1)
+    grid = torch.arange(-8, 8, dtype=torch.float64)
+    err = (Wd.unsqueeze(-1) - grid * s.unsqueeze(-1)).abs()  # (16, 8, 32, 16)
+    best = err.min(-1).values
+    q = ops.unpack_int4(codes).double().reshape(16, 8, 32)
+    mine = (Wd - q * s).abs()
+    assert torch.all(mine <= best + 1e-12)  # nearest representable value (ties either way)
+    assert torch.all(mine <= s / 2 + 1e-12)
+    assert int(q.min()) >= -8 and int(q.max()) <= 7
