@@ -444,7 +444,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": TRAFFIC_BYTES,
-            "kernel": "gemv_i4_fast<1, 2, false, 0>",
+            "kernel": "gemv_i4_fast<1, 2, 1, false, 0>",
             "kernel_us": round(i4["kernel_us"], 3),
         },
     }

@@ -47,24 +47,47 @@ constexpr int part_stride() {
   return G * kD + 2 * G;
 }
 
-// Two-halves rotation of a 64-vector held in LDS, pair (i, i+32), bf16 rounding.
-__device__ __forceinline__ void rope_pair_lds(float* v, const float* ang, int i) {
-  const float c = ang[2 * i], s = ang[2 * i + 1];
-  const float x1 = v[i], x2 = v[i + 32];
-  v[i] = bf16_to_f32(f32_to_bf16(x1 * c - x2 * s));
-  v[i + 32] = bf16_to_f32(f32_to_bf16(x2 * c + x1 * s));
+// Loads of one 16-byte chunk as 8 floats.
+__device__ __forceinline__ void unpack8(const uint4 v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = lo_bf16(w[e]);
+    f[2 * e + 1] = hi_bf16(w[e]);
+  }
 }
 
+// Two-halves RoPE of the 8 dims of chunk c of a 64-vector, given that chunk
+// (own) and chunk c ^ 4 (pair), and the 16 table floats [cos, sin] x 8 of dims
+// (c & 3) * 8 + e. Lower half: x1 c - x2 s; upper half: x2 c + x1 s. Rounded
+// to bf16, as the RoPE operator stores it.
+__device__ __forceinline__ void rope_chunk(const uint4 own, const uint4 pair, const float* ang, bool lower, float* out) {
+  float xo[8], xp[8];
+  unpack8(own, xo);
+  unpack8(pair, xp);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float c = ang[2 * e], s = ang[2 * e + 1];
+    const float r = lower ? xo[e] * c - xp[e] * s : xo[e] * c + xp[e] * s;
+    out[e] = bf16_to_f32(f32_to_bf16(r));
+  }
+}
+
+// Partials of one 64-position chunk of KV head j for its G query heads.
+// Thread -> (position rows r and r + 32 of the chunk, dims 8c..8c+7). Every
+// global load the workgroup needs (K/V rows, q and its RoPE partner chunks,
+// the table row, the new k/v) is issued right after `pos` is known, before
+// any barrier, so the kernel pays one memory round trip after the position.
 template <int G>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int NW = kDecThreads / kWave;
   constexpr int PS = part_stride<G>();
-  __shared__ float q_s[G][D];
-  __shared__ float kn_s[D];
-  __shared__ float vn_s[D];
-  __shared__ float red_s[NW][G];
-  __shared__ float o_s[G][kDecThreads / 8][D];  // per (head, position row, dim)
+  __shared__ float max_s[NW][G];
+  __shared__ float sum_s[NW][G];
+  // per (head, position row, dim); rows padded to 65 floats so the 8x8 (row, chunk) lanes of a
+  // wave writing one dim spread over the banks (a 64-float row would put 16 lanes on one bank)
+  __shared__ float o_s[G][kDecThreads / 8][D + 1];
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int s = blockIdx.x, j = blockIdx.y;
@@ -72,207 +95,198 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * kDecChunk;
-  float* part = a.part + (static_cast<size_t>(j) * a.nsplit + s) * PS;
+  if (p0 >= L) return;
+  const int c = tid & 7, r = tid >> 3;
+  const bool lower = c < 4;
+  const bool owner = pos >= p0 && pos < p0 + kDecChunk;
 
-  if (p0 < L) {
-    const float* ang = a.angles + static_cast<size_t>(pos) * D;
-    const bool owner = pos >= p0 && pos < p0 + kDecChunk;
-    for (int e = tid; e < G * D; e += kDecThreads)
-      q_s[e / D][e % D] = bf16_to_f32(a.q[static_cast<size_t>(j) * G * D + e]);
-    if (owner && tid < D) {
-      kn_s[tid] = bf16_to_f32(a.k_new[static_cast<size_t>(j) * D + tid]);
-      vn_s[tid] = bf16_to_f32(a.v_new[static_cast<size_t>(j) * D + tid]);
+  uint4 kraw[2], vraw[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int p = p0 + r + 32 * h;
+    kraw[h] = vraw[h] = make_uint4(0, 0, 0, 0);
+    if (p < pos) {
+      const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
+      kraw[h] = ld_stream16(a.k_cache + off);
+      vraw[h] = ld_stream16(a.v_cache + off);
     }
-    __syncthreads();
-    for (int t = tid; t < G * 32; t += kDecThreads) rope_pair_lds(q_s[t / 32], ang, t % 32);
-    if (owner && tid < 32) rope_pair_lds(kn_s, ang, tid);
-    __syncthreads();
-    if (owner && tid < D) {
-      const size_t off = (static_cast<size_t>(j) * a.max_len + pos) * D + tid;
-      a.k_cache[off] = f32_to_bf16(kn_s[tid]);
-      a.v_cache[off] = f32_to_bf16(vn_s[tid]);
+  }
+  const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
+  uint4 qa[G], qb[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    qa[g] = *reinterpret_cast<const uint4*>(qh + g * D + c * 8);
+    qb[g] = *reinterpret_cast<const uint4*>(qh + g * D + (c ^ 4) * 8);
+  }
+  float ang[16];
+  {
+    const float4* ap = reinterpret_cast<const float4*>(a.angles + static_cast<size_t>(pos) * D + (c & 3) * 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 t = ap[i];
+      ang[4 * i] = t.x;
+      ang[4 * i + 1] = t.y;
+      ang[4 * i + 2] = t.z;
+      ang[4 * i + 3] = t.w;
     }
+  }
+  uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
+  if (owner) {
+    kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + c * 8);
+    knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (c ^ 4) * 8);
+    vn = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + c * 8);
+  }
 
-    // thread -> position rows r and r+32 of the chunk, dims 8c..8c+7
-    const int c = tid & 7, r = tid >> 3;
-    float qv[G][8];
+  float qv[G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g) rope_chunk(qa[g], qb[g], ang, lower, qv[g]);
+  float kf[2][8], vf[2][8];
+  bool valid[2];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qv[g][e] = q_s[g][c * 8 + e];
-
-    float kf[2][8], vf[2][8];
-    bool valid[2];
+  for (int h = 0; h < 2; ++h) {
+    const int p = p0 + r + 32 * h;
+    valid[h] = p < L;
+    if (p == pos) {  // the new token: rotate k, append k/v to the caches
+      rope_chunk(kna, knb, ang, lower, kf[h]);
+      unpack8(vn, vf[h]);
+      uint32_t kw[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int p = p0 + r + 32 * h;
-      valid[h] = p < L;
-      if (p < pos) {
-        const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
-        const uint4 kk = ld_stream16(a.k_cache + off);
-        const uint4 vv = ld_stream16(a.v_cache + off);
-        const uint32_t kw[4] = {kk.x, kk.y, kk.z, kk.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          kf[h][2 * e] = lo_bf16(kw[e]);
-          kf[h][2 * e + 1] = hi_bf16(kw[e]);
-          vf[h][2 * e] = lo_bf16(vw[e]);
-          vf[h][2 * e + 1] = hi_bf16(vw[e]);
-        }
-      } else if (p == pos) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kf[h][e] = kn_s[c * 8 + e];
-          vf[h][e] = vn_s[c * 8 + e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[h][e] = vf[h][e] = 0.f;
-      }
-    }
-
-    // scores in the log2 domain; the 8 lanes of a position sum their partial dots
-    float sc[2][G];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[h][e], d);
-        d = add_dpp<0xB1>(d);   // + lane ^ 1
-        d = add_dpp<0x4E>(d);   // + lane ^ 2
-        d = add_dpp<0x141>(d);  // + lane 7-i of the 8: full 8-lane sum
-        sc[h][g] = valid[h] ? d * a.scale_log2 : -INFINITY;
-      }
-
-    // chunk maximum per head (finite: position p0 < L is always valid)
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m = wave_max(fmaxf(sc[0][g], sc[1][g]));
-      if (lane == 0) red_s[wave][g] = m;
-    }
-    __syncthreads();
-    float mloc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float m = red_s[0][g];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) m = fmaxf(m, red_s[w][g]);
-      mloc[g] = m;
-    }
-    __syncthreads();
-
-    // probabilities, their sum (one lane per position counts), and this
-    // thread's share of the unnormalised output
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float e0 = valid[0] ? exp2f(sc[0][g] - mloc[g]) : 0.f;
-      const float e1 = valid[1] ? exp2f(sc[1][g] - mloc[g]) : 0.f;
-      const float l = wave_sum(c == 0 ? e0 + e1 : 0.f);
-      if (lane == 0) red_s[wave][g] = l;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o_s[g][r][c * 8 + e] = e0 * vf[0][e] + e1 * vf[1][e];
-    }
-    __syncthreads();
-    for (int t = tid; t < G * D; t += kDecThreads) {
-      const int g = t / D, d = t % D;
-      float acc = 0.f;
-#pragma unroll 8
-      for (int rr = 0; rr < kDecThreads / 8; ++rr) acc += o_s[g][rr][d];
-      part[t] = acc;
-    }
-    if (tid < G) {
-      float l = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) l += red_s[w][tid];
-      part[G * D + tid] = mloc[tid];
-      part[G * D + G + tid] = l;
+      for (int e = 0; e < 4; ++e) kw[e] = pack_bf16x2(kf[h][2 * e], kf[h][2 * e + 1]);  // exact: already bf16 values
+      const size_t off = (static_cast<size_t>(j) * a.max_len + pos) * D + c * 8;
+      *reinterpret_cast<uint4*>(a.k_cache + off) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
+      *reinterpret_cast<uint4*>(a.v_cache + off) = vn;
+    } else {
+      unpack8(kraw[h], kf[h]);
+      unpack8(vraw[h], vf[h]);
     }
   }
 
+  // scores in the log2 domain; the 8 lanes of a position sum their partial dots
+  float sc[2][G];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[h][e], d);
+      d = add_dpp<0xB1>(d);   // + lane ^ 1
+      d = add_dpp<0x4E>(d);   // + lane ^ 2
+      d = add_dpp<0x141>(d);  // + lane 7-i of the 8: full 8-lane sum
+      sc[h][g] = valid[h] ? d * a.scale_log2 : -INFINITY;
+    }
+
+  // chunk maximum per head (finite: position p0 < L is always valid)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = wave_max(fmaxf(sc[0][g], sc[1][g]));
+    if (lane == 0) max_s[wave][g] = m;
+  }
+  __syncthreads();
+  float mloc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = max_s[0][g];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, max_s[w][g]);
+    mloc[g] = m;
+  }
+
+  // probabilities, their sum (one lane per position counts), and this
+  // thread's share of the unnormalised output
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float e0 = valid[0] ? exp2f(sc[0][g] - mloc[g]) : 0.f;
+    const float e1 = valid[1] ? exp2f(sc[1][g] - mloc[g]) : 0.f;
+    const float l = wave_sum(c == 0 ? e0 + e1 : 0.f);
+    if (lane == 0) sum_s[wave][g] = l;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o_s[g][r][c * 8 + e] = e0 * vf[0][e] + e1 * vf[1][e];
+  }
+  __syncthreads();
+  float* part = a.part + (static_cast<size_t>(j) * a.nsplit + s) * PS;
+  for (int t = tid; t < G * D; t += kDecThreads) {
+    const int g = t / D, d = t % D;
+    float acc = 0.f;
+#pragma unroll 8
+    for (int rr = 0; rr < kDecThreads / 8; ++rr) acc += o_s[g][rr][d];
+    part[t] = acc;
+  }
+  if (tid < G) {
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) l += sum_s[w][tid];
+    part[G * D + tid] = mloc[tid];
+    part[G * D + G + tid] = l;
+  }
 }
 
-// Merge of the chunk partials of one KV head (one workgroup per KV head).
+// Merge of the chunk partials of one KV head, one 1024-thread workgroup per
+// KV head. Thread -> output element t = (head, dim) of the G*64 outputs and
+// slice q of the chunks (chunks q, q + NQ, ...). Each thread folds its chunks
+// with a running maximum, loading 8 chunks per step with every load in
+// flight; the NQ slices are then combined through LDS.
+constexpr int kMergeThreads = 1024;
+
 template <int G>
-__global__ __launch_bounds__(kDecThreads) void gqa_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a) {
   constexpr int D = kD;
-  constexpr int NW = kDecThreads / kWave;
   constexpr int PS = part_stride<G>();
-  __shared__ float red_s[NW][G];
-  __shared__ float w_s[kDecThreads * G];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  constexpr int NT = G * D;                   // outputs per KV head
+  constexpr int NQ = kMergeThreads / NT;      // chunk slices
+  constexpr int B = 8;                        // chunks per step per thread
+  __shared__ float m_s[kMergeThreads], l_s[kMergeThreads], o_s[kMergeThreads];
+  const int tid = threadIdx.x, t = tid % NT, q = tid / NT, g = t / D;
   const int j = blockIdx.x;
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
   const int nact = (pos + kDecChunk) / kDecChunk;
   const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
-  // global maximum and sum per head: splits strided over the threads
-  float mg[G], lg[G];
+  float M = -INFINITY, Ls = 0.f, acc = 0.f;
+  for (int k0 = q; k0 < nact; k0 += NQ * B) {
+    float mb[B], lb[B], ob[B];
 #pragma unroll
-  for (int g = 0; g < G; ++g) mg[g] = -INFINITY;
-  for (int k = tid; k < nact; k += kDecThreads)
-#pragma unroll
-    for (int g = 0; g < G; ++g) mg[g] = fmaxf(mg[g], base[k * PS + G * D + g]);
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m = wave_max(mg[g]);
-    if (lane == 0) red_s[wave][g] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = red_s[0][g];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, red_s[w][g]);
-    mg[g] = m;
-    lg[g] = 0.f;
-  }
-  __syncthreads();
-  for (int k = tid; k < nact; k += kDecThreads)
-#pragma unroll
-    for (int g = 0; g < G; ++g) lg[g] += base[k * PS + G * D + G + g] * exp2f(base[k * PS + G * D + g] - mg[g]);
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float l = wave_sum(lg[g]);
-    if (lane == 0) red_s[wave][g] = l;
-  }
-  __syncthreads();
-  float inv[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float l = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) l += red_s[w][g];
-    inv[g] = 1.f / l;
-  }
-  // outputs: per-split weights staged in LDS (slabs of kDecThreads splits),
-  // partial outputs read as independent loads
-  constexpr int OPT = (G * D + kDecThreads - 1) / kDecThreads;  // outputs per thread
-  float acc[OPT];
-#pragma unroll
-  for (int i = 0; i < OPT; ++i) acc[i] = 0.f;
-  for (int k0 = 0; k0 < nact; k0 += kDecThreads) {
-    const int kn = min(kDecThreads, nact - k0);
-    __syncthreads();
-    if (tid < kn)
-#pragma unroll
-      for (int g = 0; g < G; ++g) w_s[tid * G + g] = exp2f(base[(k0 + tid) * PS + G * D + g] - mg[g]);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < OPT; ++i) {
-      const int t = tid + i * kDecThreads, g = t / D;
-      if (t >= G * D) break;
-      float o = acc[i];
-#pragma unroll 8
-      for (int k = 0; k < kn; ++k) o = fmaf(base[(k0 + k) * PS + t], w_s[k * G + g], o);
-      acc[i] = o;
+    for (int b = 0; b < B; ++b) {
+      const int k = k0 + b * NQ;
+      mb[b] = -INFINITY;
+      lb[b] = ob[b] = 0.f;
+      if (k < nact) {
+        const float* pk = base + static_cast<size_t>(k) * PS;
+        mb[b] = pk[G * D + g];
+        lb[b] = pk[G * D + G + g];
+        ob[b] = pk[t];
+      }
     }
-  }
+    float bm = M;
 #pragma unroll
-  for (int i = 0; i < OPT; ++i) {
-    const int t = tid + i * kDecThreads, g = t / D;
-    if (t < G * D) a.out[static_cast<size_t>(j) * G * D + t] = f32_to_bf16(acc[i] * inv[g]);
+    for (int b = 0; b < B; ++b) bm = fmaxf(bm, mb[b]);  // finite: chunk k0 < nact is active
+    const float keep = exp2f(M - bm);                   // 0 on the first step
+    acc *= keep;
+    Ls *= keep;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float w = exp2f(mb[b] - bm);  // 0 for the chunks past nact
+      acc = fmaf(w, ob[b], acc);
+      Ls = fmaf(w, lb[b], Ls);
+    }
+    M = bm;
+  }
+  m_s[tid] = M;
+  l_s[tid] = Ls;
+  o_s[tid] = acc;
+  __syncthreads();
+  if (q == 0) {
+    float Mx = M;  // slice 0 always holds chunk 0
+#pragma unroll
+    for (int qq = 1; qq < NQ; ++qq) Mx = fmaxf(Mx, m_s[qq * NT + t]);
+    float lt = 0.f, ot = 0.f;
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq) {
+      const float w = exp2f(m_s[qq * NT + t] - Mx);  // 0 for an empty slice
+      lt = fmaf(w, l_s[qq * NT + t], lt);
+      ot = fmaf(w, o_s[qq * NT + t], ot);
+    }
+    a.out[static_cast<size_t>(j) * NT + t] = f32_to_bf16(ot / lt);
   }
 }
 
@@ -447,7 +461,9 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
   IRON_REQUIRE(pos_dev || (pos >= 0 && pos < max_len && pos < angle_rows),
                "iron_gqa_decode: pos=%d outside the cache (max_len=%d) or angle table (%d rows)", pos, max_len,
                angle_rows);
-  IRON_REQUIRE(aligned16(k_cache) && aligned16(v_cache), "iron_gqa_decode: caches must be 16-byte aligned");
+  IRON_REQUIRE(aligned16(q) && aligned16(k_new) && aligned16(v_new) && aligned16(k_cache) && aligned16(v_cache) &&
+                   aligned16(angles),
+               "iron_gqa_decode: q, k_new, v_new, the caches and the angle table must be 16-byte aligned");
   IRON_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "iron_gqa_decode: workspace must be 256-byte aligned");
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -466,23 +482,23 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
   a.scale_log2 = scale * 1.4426950408889634f;
   dim3 grid(a.nsplit, n_kv_heads), block(kDecThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 cgrid(n_kv_heads);
+  dim3 cgrid(n_kv_heads), cblock(kMergeThreads);
   switch (G) {
     case 1:
       IRON_LAUNCH((gqa_decode_kernel<1>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<1>), cgrid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<1>), cgrid, cblock, 0, s, a);
       break;
     case 2:
       IRON_LAUNCH((gqa_decode_kernel<2>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<2>), cgrid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<2>), cgrid, cblock, 0, s, a);
       break;
     case 4:
       IRON_LAUNCH((gqa_decode_kernel<4>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<4>), cgrid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<4>), cgrid, cblock, 0, s, a);
       break;
     default:
       IRON_LAUNCH((gqa_decode_kernel<8>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, block, 0, s, a);
+      IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, cblock, 0, s, a);
       break;
   }
   return check_launch("gqa_decode");

@@ -42,6 +42,7 @@ struct GemvArgs {
   int M, K;
   float eps;
   int epi;
+  int xcd;  // 1: XCD-contiguous row order (xcd_block)
 };
 
 // Normalises the 8 bf16 values of an x chunk: bf16(x * inv * w).
@@ -105,12 +106,22 @@ __device__ __forceinline__ void publish_key(unsigned long long* keys, size_t key
   }
 }
 
+// Workgroup index -> logical tile. With `enable` (and a grid that is a
+// multiple of 8), each XCD (workgroup b runs on XCD b % 8) owns one
+// contiguous eighth of the rows: its weight rows are adjacent in HBM and every
+// 64-byte line of y is written from one L2 only.
+__device__ __forceinline__ int xcd_block(int enable) {
+  const int nb = gridDim.x, b = blockIdx.x;
+  return (!enable || (nb & 7)) ? b : (b & 7) * (nb >> 3) + (b >> 3);
+}
+
 // Fast path: K == 512*U exactly; each lane holds U chunks of W (and W2) in
 // flight. One wave per output row.
 template <int U, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tile = xcd_block(a.xcd);
+  const int row = tile * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const bool active = row < a.M;  // uniform per wave
   if (!active && !a.keys) return;  // without keys the kernel has no block barrier
@@ -158,14 +169,15 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
     if (lane == 0) v = finish_row(a.resid, a.epi, a.y, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
-  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + blockIdx.x, key);
+  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + tile, key);
 }
 
 // Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mode) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int tile = xcd_block(a.xcd);
+  const int row = tile * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const bool active = row < a.M;
   if (!active && !a.keys) return;
@@ -208,7 +220,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mo
     if (lane == 0) v = finish_row(a.resid, a.epi, a.y, static_cast<size_t>(b) * a.M + row, row, acc, acc2, PAIR);
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
-  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + blockIdx.x, key);
+  if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + tile, key);
 }
 
 template <int U, bool PAIR>
@@ -267,6 +279,7 @@ struct I4Args {
   int epi;
   uint32_t magic;  // 0x43084308 signed two's-complement nibbles, 0x43004300 unsigned
   float offset;    // 136 signed, 128 unsigned
+  int xcd;         // 1: XCD-contiguous row order (xcd_block)
 };
 
 // x chunk of one group (32 bf16) rearranged into the nibble-pair order:
@@ -313,19 +326,25 @@ __device__ __forceinline__ float i4_group_dot(uint4 c, const XGroup& g, uint32_t
   return acc;
 }
 
-// Fast path: K == 2048*GPL (every lane owns exactly GPL groups of a row) and
-// M % R == 0 (R rows per wave, sharing the x preparation).
-template <int GPL, int R, bool PAIR, int NM>
+// Fast path: K == 2048*GPL*KS. The 4 waves of a workgroup form 4/KS row
+// groups of R rows; the KS waves of a row group split K, each lane owning GPL
+// groups of 32 per row, and their partial sums meet in LDS. R rows of one
+// wave share the x preparation.
+template <int GPL, int R, int KS, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-  const bool active = row0 < a.M;  // uniform per wave
-  if (!active && !a.keys) return;
-  unsigned long long key = 0;
+  static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int tile = xcd_block(a.xcd);
+  const int rg = wave / KS, kp = wave % KS;
+  const int row0 = (tile * (4 / KS) + rg) * R;
+  const bool active = row0 < a.M;  // uniform per row group
+  if (KS == 1 && !active && !a.keys) return;
+  constexpr int G = GPL * kWave * KS;                   // groups per row
+  constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
+  const int g0 = kp * GPL * kWave + lane;               // this lane's first group
+  float part[R][2];
+  float inv = 1.f, ss = 0.f;
   if (active) {
-    constexpr int G = GPL * kWave;
-    constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
-
     // Weight loads first, so they are in flight while x is prepared.
     uint4 cw[R][GPL], cw2[R][GPL];
     uint16_t sc[R][GPL], sc2[R][GPL];
@@ -334,7 +353,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       const size_t row = static_cast<size_t>(row0 + r);
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
-        const int g = lane + j * kWave;
+        const int g = g0 + j * kWave;
         cw[r][j] = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
         sc[r][j] = a.scales[row * G + g];
         if (PAIR) {
@@ -349,22 +368,30 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
     for (int j = 0; j < GPL; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xr[j][q] = xv[(lane + j * kWave) * 4 + q];
-    float inv = 1.f;
+      for (int q = 0; q < 4; ++q) xr[j][q] = xv[(g0 + j * kWave) * 4 + q];
     if (NM != NORM_NONE) {
-      float ss = 0.f;
 #pragma unroll
       for (int j = 0; j < GPL; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[j][q], ss);
-      inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+      ss = wave_sum(ss);
+      if (KS == 1) inv = rsqrtf(ss / static_cast<float>(a.K) + a.eps);
     }
     if (NM == NORM_WEIGHT) {
+      if (KS > 1) {  // the full sum of squares is needed before the products
+        __shared__ float ss_s[4];
+        if (lane == 0) ss_s[wave] = ss;
+        __syncthreads();
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) t += ss_s[rg * KS + k];
+        inv = rsqrtf(t / static_cast<float>(a.K) + a.eps);
+      }
       const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w);
 #pragma unroll
       for (int j = 0; j < GPL; ++j)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) xr[j][q] = normalize_chunk(xr[j][q], nw[(lane + j * kWave) * 4 + q], inv);
+        for (int q = 0; q < 4; ++q) xr[j][q] = normalize_chunk(xr[j][q], nw[(g0 + j * kWave) * 4 + q], inv);
     }
     XGroup xg[GPL];
 #pragma unroll
@@ -382,21 +409,55 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
           acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
         }
       }
-      float t = wave_sum(acc);
-      float t2 = PAIR ? wave_sum(acc2) : 0.f;
+      part[r][0] = wave_sum(acc);
+      part[r][1] = PAIR ? wave_sum(acc2) : 0.f;
+    }
+  }
+  if (KS > 1) {  // K-split partners meet in LDS; the kp == 0 wave finishes the rows
+    __shared__ float p_s[4][R][2];
+    __shared__ float q_s[4];
+    if (lane == 0 && active) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        p_s[wave][r][0] = part[r][0];
+        p_s[wave][r][1] = part[r][1];
+      }
+      q_s[wave] = ss;
+    }
+    __syncthreads();
+    if (kp != 0 || !active) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int k = 1; k < KS; ++k) {
+        part[r][0] += p_s[wave + k][r][0];
+        part[r][1] += p_s[wave + k][r][1];
+      }
+    if (NM == NORM_SCALE) {
+      float t = ss;
+#pragma unroll
+      for (int k = 1; k < KS; ++k) t += q_s[wave + k];
+      inv = rsqrtf(t / static_cast<float>(a.K) + a.eps);
+    }
+  }
+  unsigned long long key = 0;
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float t = part[r][0], t2 = part[r][1];
       if (NM == NORM_SCALE) {
         t *= inv;
         t2 *= inv;
       }
       float v = 0.f;
       if (lane == 0) v = finish_row(a.resid, a.epi, a.y, row0 + r, row0 + r, t, t2, PAIR);
-      if (a.keys) {
+      if (KS == 1 && a.keys) {
         const unsigned long long k = argmax_key(__shfl(v, 0, kWave), row0 + r);
         key = k > key ? k : key;
       }
     }
   }
-  if (a.keys) publish_key(a.keys, blockIdx.x, key);
+  if (KS == 1 && a.keys) publish_key(a.keys, tile, key);
 }
 
 // Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
@@ -447,29 +508,45 @@ __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) 
   if (a.keys) publish_key(a.keys, blockIdx.x, key);
 }
 
-template <int GPL, int R, bool PAIR>
+template <int GPL, int R, int KS, bool PAIR>
 void launch_i4_fast(const I4Args& a, int norm_mode, hipStream_t s) {
-  dim3 grid((a.M / R + 3) / 4), block(256);
+  const int rows_per_block = R * 4 / KS;
+  dim3 grid((a.M + rows_per_block - 1) / rows_per_block), block(256);
   switch (norm_mode) {
-    case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_WEIGHT>), grid, block, 0, s, a); break;
-    case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_SCALE>), grid, block, 0, s, a); break;
-    default: IRON_LAUNCH((gemv_i4_fast<GPL, R, PAIR, NORM_NONE>), grid, block, 0, s, a); break;
+    case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_WEIGHT>), grid, block, 0, s, a); break;
+    case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_SCALE>), grid, block, 0, s, a); break;
+    default: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_NONE>), grid, block, 0, s, a); break;
   }
 }
 
 template <bool PAIR>
 int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
-  const int gpl = (a.K % 2048 == 0) ? a.K / 2048 : 0;
-  // Two rows per wave when there are enough rows to keep >= 4 waves per SIMD
-  // (not with argmax keys, which are defined per 4 rows).
-  const bool r2 = !PAIR && !a.keys && a.M % 2 == 0 && a.M >= 8192;
-  switch (gpl) {
-    case 1:
-      if (r2) launch_i4_fast<1, 2, PAIR>(a, norm_mode, s);
-      else launch_i4_fast<1, 1, PAIR>(a, norm_mode, s);
+  // Argmax keys are defined per 4 rows: one row per wave, no K split.
+  if (a.keys) {
+    if (a.K == 2048) launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
+    else IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
+    return check_launch("gemv_i4g32");
+  }
+  // Two rows per wave share x when there are enough rows to keep >= 4 waves
+  // per SIMD; longer rows are split over 2 or 4 waves.
+  const bool r2 = !PAIR && a.M % 2 == 0 && a.M >= 8192;
+  switch (a.K) {
+    case 2048:
+      if (r2) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
+      else launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
       break;
-    case 2: launch_i4_fast<2, 1, PAIR>(a, norm_mode, s); break;
-    case 4: launch_i4_fast<4, 1, PAIR>(a, norm_mode, s); break;
+    case 4096:  // a workgroup is 2 row groups: both must be inside M
+      if (a.M % 2 == 0) {
+        launch_i4_fast<1, 1, 2, PAIR>(a, norm_mode, s);
+        break;
+      }
+      [[fallthrough]];
+    case 8192:
+      if (a.K == 8192) {
+        launch_i4_fast<1, 1, 4, PAIR>(a, norm_mode, s);
+        break;
+      }
+      [[fallthrough]];
     default:
       IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
       break;
@@ -548,7 +625,8 @@ extern "C" int iron_gemv_bf16(const void* W, const void* x, void* y, int M, int 
   IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16: bad epilogue %d",
                epilogue);
   GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x),
-             static_cast<uint16_t*>(y), nullptr, nullptr, nullptr, M, K, 0.f, epilogue};
+             static_cast<uint16_t*>(y), nullptr, nullptr, nullptr, M, K, 0.f, epilogue,
+             0};  // round-robin rows: the XCD-contiguous order measured slower for bf16 rows
   return launch_gemv_bf16<false>(a, NORM_NONE, batches, static_cast<hipStream_t>(stream));
 }
 
@@ -582,7 +660,8 @@ extern "C" int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x
              M,
              K,
              eps,
-             epilogue};
+             epilogue,
+             0};  // round-robin rows (see iron_gemv_bf16)
   hipStream_t s = static_cast<hipStream_t>(stream);
   return W2 ? launch_gemv_bf16<true>(a, norm_mode, 1, s) : launch_gemv_bf16<false>(a, norm_mode, 1, s);
 }
@@ -625,7 +704,8 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
            eps,
            epilogue,
            is_signed ? 0x43084308u : 0x43004300u,
-           is_signed ? 136.f : 128.f};
+           is_signed ? 136.f : 128.f,
+           1};  // XCD-contiguous rows: measured faster for every int4 shape of the decode step
   hipStream_t s = static_cast<hipStream_t>(stream);
   return codes2 ? launch_gemv_i4<true>(a, norm_mode, s) : launch_gemv_i4<false>(a, norm_mode, s);
 }

@@ -82,10 +82,19 @@ __global__ __launch_bounds__(1024) void select_embed_kernel(const unsigned long 
                                                             int* history, int history_cap) {
   __shared__ unsigned long long ks[16];
   __shared__ int tok_s;
+  const int p = pos ? *pos : 0;  // independent of the keys: in flight with them
+  // 16 keys per thread per step, all loads issued before the first compare
+  constexpr int U = 16;
   unsigned long long best = 0;
-  for (int i = threadIdx.x; i < n_keys; i += 1024) {
-    const unsigned long long k = keys[i];
-    best = k > best ? k : best;
+  for (int base = 0; base < n_keys; base += 1024 * U) {
+    unsigned long long k[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * 1024 + static_cast<int>(threadIdx.x);
+      k[u] = i < n_keys ? keys[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) best = k[u] > best ? k[u] : best;
   }
   for (int off = 32; off > 0; off >>= 1) {
     const unsigned long long o = __shfl_xor(best, off, kWave);
@@ -101,7 +110,6 @@ __global__ __launch_bounds__(1024) void select_embed_kernel(const unsigned long 
     tok_s = tok;
     token_out[0] = tok;
     if (pos) {
-      const int p = *pos;
       if (history && p >= 0 && p < history_cap) history[p] = tok;
       *pos = p + 1;
     }

@@ -262,3 +262,51 @@ def test_argmax_keys_and_select(gpu, int4, M):
     expect = int(torch.argmax(y.cpu().float()))
     assert int(tok.item()) == expect and int(hist[5].item()) == expect and int(pos.item()) == 6
     assert torch.equal(xo.cpu(), table[expect].cpu())
+
+
+@pytest.mark.parametrize("M,K", [(2048, 8192), (96, 8192), (64, 4096), (65, 4096), (512, 2048), (8192, 2048), (40, 1024)])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("pair", [False, True])
+def test_gemv_int4_fused_modes(gpu, M, K, mode, pair):
+    """iron_gemv_i4g32_fused over the row/K splits the launcher picks (one wave
+    per row, two rows per wave, K split over 2 or 4 waves, generic), each norm
+    mode, with and without the SwiGLU pair, with a residual. Bar: max-abs 2e-2,
+    rel-L2 1e-2 against float64 on the exact weights q*s (the kernel never
+    rounds a weight to bf16), where an output above ~4 in magnitude may instead
+    differ by up to 2 bf16 ulps (its rounding step alone exceeds 2e-2); mode 1
+    rounds the normalised x to bf16 first, as the RMSNorm operator stores it."""
+    from iron_amd import _lib
+
+    g = torch.Generator().manual_seed(M * 131 + K + 7 * mode + int(pair))
+    W = (torch.randn(M, K, generator=g) * 0.02).to(BF16)
+    W2 = (torch.randn(M, K, generator=g) * 0.02).to(BF16)
+    x = torch.randn(K, generator=g).to(BF16)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    resid = torch.randn(M, generator=g).to(BF16)
+    c, s = (t.to(gpu) for t in ops.quantize_int4_g32(W))
+    c2, s2 = (t.to(gpu) for t in ops.quantize_int4_g32(W2)) if pair else (None, None)
+    y = torch.empty(M, dtype=BF16, device=gpu)
+    xd, nwd, rd = x.to(gpu), nw.to(gpu), resid.to(gpu)
+    _lib.call("iron_gemv_i4g32_fused", c.data_ptr(), s.data_ptr(), c2.data_ptr() if pair else None,
+              s2.data_ptr() if pair else None, xd.data_ptr(), y.data_ptr(), M, K, 1, mode,
+              nwd.data_ptr() if mode == 1 else None, 1e-5, rd.data_ptr(), 0, None, _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    def exact(cc, ss):
+        return ops.unpack_int4(cc.cpu()).double() * ss.cpu().double().repeat_interleave(32, 1)
+
+    xf = x.double()
+    inv = torch.rsqrt((xf * xf).mean() + 1e-5)
+    xn = (x.float() * inv.float() * nw.float()).to(BF16).double() if mode == 1 else xf
+    t = exact(c, s) @ xn
+    if mode == 2:
+        t = t * inv
+    if pair:
+        t2 = exact(c2, s2) @ xn
+        if mode == 2:
+            t2 = t2 * inv
+        t = torch.nn.functional.silu(t) * t2
+    ref = t + resid.double()
+    max_abs, rel_l2 = ops.max_abs_rel_l2(y, ref)
+    assert rel_l2 <= 1e-2, rel_l2
+    bad = ops.within_bf16_ulps(y, ref, n_ulp=2.0, atol=2e-2)
+    assert not bad, (max_abs, [(i, float(y[i]), float(ref[i])) for i in bad[:5]])
