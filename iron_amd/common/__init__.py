@@ -6,8 +6,11 @@ from .base import (
     MLIROperator,
     CompositeOperator,
     AIERuntimeArgSpec,
+    set_reference_provider,
+    get_reference_provider,
 )
 from .context import AIEContext
+from .sequence import OperatorSequence, Tolerance
 
 __all__ = [
     "AIEOperatorBase",
@@ -16,4 +19,8 @@ __all__ = [
     "CompositeOperator",
     "AIERuntimeArgSpec",
     "AIEContext",
+    "OperatorSequence",
+    "Tolerance",
+    "set_reference_provider",
+    "get_reference_provider",
 ]

@@ -60,6 +60,22 @@ class AIERuntimeArgSpec:
         return self.numel * torch.empty((), dtype=self.dtype).element_size()
 
 
+# Callable (operator, *cpu_tensors) -> cpu tensor behind AIEOperatorBase.reference().
+_reference_provider: Callable[..., Any] | None = None
+
+
+def set_reference_provider(fn: Callable[..., Any] | None) -> None:
+    """Register (or clear, with None) the function that computes operators'
+    CPU references, used by reference() and the compare/reference dispatch
+    modes of OperatorSequence."""
+    global _reference_provider
+    _reference_provider = fn
+
+
+def get_reference_provider() -> Callable[..., Any] | None:
+    return _reference_provider
+
+
 class AIEOperatorBase(ABC):
     """Base of every operator (name kept from iron/common/base.py:33)."""
 
@@ -96,11 +112,22 @@ class AIEOperatorBase(ABC):
     def get_callable(self) -> Callable[..., Any]: ...
 
     def reference(self, *inputs):
-        """CPU references are test infrastructure (oracle/), not part of the library."""
-        raise NotImplementedError(
-            f"{type(self).__name__}.reference(): CPU references live in the test oracle "
-            "(oracle/ops.py); the library ships only the HIP path"
-        )
+        """CPU result of this operator on CPU tensors (base.py:155-157 in the
+        reference). The library ships no CPU path: the result comes from the
+        provider registered with ``set_reference_provider`` (the tests register
+        their CPU oracle); without one this raises."""
+        if _reference_provider is None:
+            raise NotImplementedError(
+                f"{type(self).__name__}.reference(): no reference provider is registered; "
+                "the library ships only the HIP path (register one with "
+                "iron_amd.common.set_reference_provider)"
+            )
+        return _reference_provider(self, *inputs)
+
+    def reference_tolerance(self):
+        """Tolerance a compare-mode OperatorSequence holds this operator to
+        (None: the dispatch's fallback)."""
+        return None
 
 
 def _serialize_param(v: object) -> str:

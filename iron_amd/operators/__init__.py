@@ -20,6 +20,8 @@ _OPERATOR_MODULES = {
     "RoPE": "rope",
     "SiLU": "silu",
     "Softmax": "softmax",
+    "SwiGLUDecode": "swiglu_decode",
+    "SwiGLUPrefill": "swiglu_prefill",
 }
 
 _SUBPACKAGES: tuple = ("flm",)

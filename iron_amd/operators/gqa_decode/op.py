@@ -10,7 +10,9 @@ kernel (iron_gqa_decode); semantics are the CPU golden's
 Arg spec: q (H, D), k_new (Hkv, D), v_new (Hkv, D), k_cache and v_cache
 (Hkv, max_len, D) inout, angles (angle_rows, D) fp32 [cos, sin] interleaved,
 out (H, D). The position comes from ``set_position(pos)`` (host int) or
-``position_tensor`` (a device int32 read at run time, for graph replay).
+``position_tensor`` (a device int32 read at run time, for graph replay);
+inside an OperatorSequence, ``position_parameter`` names the runtime
+parameter that supplies it.
 The workspace is allocated by the operator (zeroed once) per device.
 """
 
@@ -31,6 +33,7 @@ class GQADecode(HIPOperator):
     max_len: int
     angle_rows: int | None = None
     scale: float | None = field(default=None, repr=False)
+    position_parameter: str | None = field(default=None, repr=False)
     context: object = field(default=None, repr=False)
 
     def __post_init__(self):

@@ -19,6 +19,12 @@ if str(ROOT) not in sys.path:
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: test needs an MI355X GPU")
     config.addinivalue_line("markers", "extensive: extensive test suite")
+    # operators' reference() in the tests is the CPU oracle
+    from iron_amd.common import set_reference_provider
+
+    from tests import oracle_provider
+
+    set_reference_provider(oracle_provider.reference)
 
 
 @pytest.fixture(scope="session")
