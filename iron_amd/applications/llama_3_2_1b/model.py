@@ -190,7 +190,8 @@ class LlamaHIP:
 
         self.embed = w["model.embed_tokens.weight"]
         self.final_norm = w["model.norm.weight"]
-        self.head = Linear(fold(self.embed, self.final_norm), cfg.head_int4, s)
+        # tied head (the reference's model) unless the weights carry their own lm_head
+        self.head = Linear(fold(w.get("lm_head.weight", self.embed), self.final_norm), cfg.head_int4, s)
         self.layers = []
         for i in range(cfg.n_layers):
             p = f"model.layers.{i}."
