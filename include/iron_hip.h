@@ -214,6 +214,34 @@ int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K
  * row-major B (the role of iron/operators/transpose/op.py:18-120). */
 int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream);
 
+/* ------------------------------------------------------ data movement ---- */
+
+/* out[b] (cols, rows) = in[b] (rows, cols)^T for b < batches (matrices back
+ * to back), bf16. Replaces Transpose.get_callable() -> (in, out) of
+ * iron/operators/transpose/op.py:16-120 (num_batches). */
+int iron_transpose_batched_bf16(const void* in, void* out, int rows, int cols, int batches, void* stream);
+
+/* Repeat-interleave of rows: out row r*repeat+k = x row r (k < repeat), rows of
+ * row_bytes bytes (any element type). Replaces Repeat.get_callable() ->
+ * (in, out) of iron/operators/repeat/op.py:15-70. */
+int iron_repeat_rows(const void* x, void* out, long long rows, long long row_bytes, int repeat, void* stream);
+
+/* Strided copy: out[dst(k)] = in[src(k)] for every element k of two 1-4 D
+ * access patterns (sizes, strides, offset, in elements of elem_bytes bytes),
+ * split over `channels` along each pattern's last dimension of size >= 1 as
+ * the reference splits them (strided_copy/reference.py:9-75). Elements of out
+ * outside the output pattern are left as they were. in_addend_dev /
+ * out_addend_dev (optional device int32) add a run-time element offset (the
+ * *_offset_parameter of a sequence); without them the host checks the
+ * patterns against in_len / out_len (elements), with them the kernel skips
+ * out-of-range elements. Replaces StridedCopy.get_callable() -> (in, out) of
+ * iron/operators/strided_copy/op.py:15-110. */
+int iron_strided_copy(const void* in, void* out, int elem_bytes, long long in_len, long long out_len, int ndim_in,
+                      const long long* in_sizes, const long long* in_strides, long long in_offset,
+                      const int* in_addend_dev, int ndim_out, const long long* out_sizes,
+                      const long long* out_strides, long long out_offset, const int* out_addend_dev, int channels,
+                      void* stream);
+
 /* --------------------------------------------------------- Llama glue ---- */
 
 /* out[i] = table[ids[i]] (rows of dim bf16; zeros for ids outside [0,vocab)).

@@ -442,6 +442,12 @@ def _runtime_parameters(op):
     name = getattr(op, "position_parameter", None)
     if name:
         out.append((name, lambda t, op=op: setattr(op, "position_tensor", t)))
+    name = getattr(op, "input_offset_parameter", None)
+    if name:
+        out.append((name, lambda t, op=op: setattr(op, "_in_addend_dev", t)))
+    name = getattr(op, "output_offset_parameter", None)
+    if name:
+        out.append((name, lambda t, op=op: setattr(op, "_out_addend_dev", t)))
     return out
 
 

@@ -22,6 +22,9 @@ _OPERATOR_MODULES = {
     "Softmax": "softmax",
     "SwiGLUDecode": "swiglu_decode",
     "SwiGLUPrefill": "swiglu_prefill",
+    "Transpose": "transpose",
+    "StridedCopy": "strided_copy",
+    "Repeat": "repeat",
 }
 
 _SUBPACKAGES: tuple = ("flm",)

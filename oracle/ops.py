@@ -499,3 +499,52 @@ def max_abs_rel_l2(out, ref):
     r = ref.detach().double().cpu().reshape(-1)
     d = o - r
     return float(d.abs().max()), float(d.norm() / max(r.norm(), 1e-30))
+
+
+# ------------------------------------------------------------- data movement
+def transpose_reference(x, M, N):
+    """Each (M, N) matrix of x transposed (transpose/reference.py:7-10)."""
+    return x.reshape(-1, M, N).transpose(-2, -1).contiguous()
+
+
+def repeat_reference(x, repeat):
+    """Repeat-interleave along dim 0 (repeat/reference.py:7-9)."""
+    return x.repeat_interleave(repeat, dim=0)
+
+
+def _pad_to_4d(sizes, strides):
+    return [1] * (4 - len(sizes)) + list(sizes), [0] * (4 - len(strides)) + list(strides)
+
+
+def _tap_offsets(sizes, strides, offset):
+    grids = np.meshgrid(*[np.arange(s) for s in sizes], indexing="ij")
+    flat = np.full(grids[0].shape, offset, dtype=np.int64)
+    for grid, stride in zip(grids, strides):
+        flat = flat + grid * stride
+    return flat.reshape(-1)
+
+
+def _channel_offsets(sizes, strides, offset, channels):
+    sizes, strides = _pad_to_4d(sizes, strides)
+    highest = max(i for i, s in enumerate(sizes) if s >= 1)
+    per = sizes[highest] // channels
+    split = sizes[:highest] + [per] + sizes[highest + 1 :]
+    return [_tap_offsets(split, strides, offset + c * per * strides[highest]) for c in range(channels)]
+
+
+def strided_copy_reference(input_flat, input_sizes, input_strides, input_offset, output_buffer_size, output_sizes,
+                           output_strides, output_offset, num_aie_channels=1, input_offset_addend=0,
+                           output_offset_addend=0, out=None):
+    """Gather by the input pattern, scatter by the output pattern, channel by
+    channel (strided_copy/reference.py:9-75). The reference starts from a zero
+    output; ``out`` gives the prior contents instead (elements outside the
+    output pattern keep them, as on the device).
+    PINNED BY: nested-loop brute force and the KV-cache append identity."""
+    src = _channel_offsets(input_sizes, input_strides, input_offset + input_offset_addend, num_aie_channels)
+    dst = _channel_offsets(output_sizes, output_strides, output_offset + output_offset_addend, num_aie_channels)
+    res = torch.zeros(int(output_buffer_size), dtype=input_flat.dtype) if out is None else out.clone()
+    for s, d in zip(src, dst):
+        if len(s) != len(d):
+            raise ValueError(f"tap element counts differ ({len(s)} vs {len(d)})")
+        res[torch.from_numpy(d)] = input_flat[torch.from_numpy(s)]
+    return res

@@ -210,3 +210,64 @@ def test_swiglu_golden_chain_consistent():
     assert torch.allclose(d["left"].double(), left, rtol=2**-7, atol=1e-3 * left.abs().max().item())
     inter = d["left_swished"].double() * d["right"].double()
     assert torch.allclose(d["intermediate"].double(), inter, rtol=2**-7, atol=1e-6)
+
+
+def _strided_brute(inp, isz, ist, ioff, out_len, osz, ost, ooff, channels):
+    """Nested loops over each channel's split pattern (no numpy meshgrid)."""
+    import itertools
+
+    def pad(sz, st):
+        return [1] * (4 - len(sz)) + list(sz), [0] * (4 - len(st)) + list(st)
+
+    def offsets(sz, st, off):
+        sz, st = pad(sz, st)
+        hi = max(i for i, s in enumerate(sz) if s >= 1)
+        per = sz[hi] // channels
+        res = []
+        for c in range(channels):
+            split = sz[:hi] + [per] + sz[hi + 1 :]
+            base = off + c * per * st[hi]
+            chan = []
+            for idx in itertools.product(*[range(s) for s in split]):
+                chan.append(base + sum(i * s for i, s in zip(idx, st)))
+            res.append(chan)
+        return res
+
+    out = torch.zeros(out_len, dtype=inp.dtype)
+    for s, d in zip(offsets(isz, ist, ioff), offsets(osz, ost, ooff)):
+        for a, b in zip(s, d):
+            out[b] = inp[a]
+    return out
+
+
+@pytest.mark.parametrize("channels", [1, 2, 4])
+def test_strided_copy_matches_brute_force(channels):
+    g = torch.Generator().manual_seed(channels)
+    inp = torch.rand(512, generator=g).to(torch.bfloat16)
+    cases = [
+        ([8, 16], [16, 1], 0, 1024, [8, 1, 16], [64, 0, 1], 5),
+        ([4, 8, 8], [64, 1, 8], 3, 600, [4, 64], [128, 1], 40),  # permuted gather
+        ([256], [2], 0, 256, [256], [1], 0),
+    ]
+    for isz, ist, ioff, olen, osz, ost, ooff in cases:
+        ref = ops.strided_copy_reference(inp, isz, ist, ioff, olen, osz, ost, ooff, num_aie_channels=channels)
+        assert torch.equal(ref, _strided_brute(inp, isz, ist, ioff, olen, osz, ost, ooff, channels))
+
+
+def test_strided_copy_kv_append_identity():
+    """The KV-cache write of llama_npu.py:311-323: cache[:, slot, :] = x."""
+    n_kv, hd, seq, slot = 8, 64, 32, 7
+    x = torch.randn(n_kv, hd).to(torch.bfloat16)
+    cache = torch.randn(n_kv, seq, hd).to(torch.bfloat16)
+    out = ops.strided_copy_reference(x.reshape(-1), [n_kv, hd], [hd, 1], 0, n_kv * seq * hd, [1, n_kv, hd],
+                                     [0, seq * hd, 1], 0, output_offset_addend=slot * hd, out=cache.reshape(-1))
+    expect = cache.clone()
+    expect[:, slot, :] = x
+    assert torch.equal(out.reshape(n_kv, seq, hd), expect)
+
+
+def test_repeat_and_transpose_references():
+    x = torch.arange(12.0).reshape(3, 4)
+    assert ops.repeat_reference(x, 2).tolist() == [r for r in x.tolist() for _ in range(2)]
+    t = ops.transpose_reference(torch.arange(24.0), 4, 6)
+    assert torch.equal(t[0], torch.arange(24.0).reshape(4, 6).T)
