@@ -210,6 +210,20 @@ int iron_attention_prefill(const void* q, const void* k, const void* v, void* ou
 int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K, long long ldc, int epilogue,
                       int has_clamp, float clamp_lo, float clamp_hi, void* stream);
 
+/* Split-K form of iron_gemm_bf16_nt for shapes whose 128x128 output tiles
+ * cannot fill the GPU (prefill projections at short prompts): the K range is
+ * cut into `splits` equal parts (splits must divide K/64), each writes fp32
+ * partial sums to `workspace` (splits*M*N*4 bytes, 16-byte aligned), and a
+ * second kernel sums them in order and applies the same bf16 rounding,
+ * epilogue and clamp. Deterministic. iron_gemm_splitk_choose returns the
+ * split count this library uses for (M, N, K) (1: no split);
+ * iron_gemm_splitk_workspace_bytes the workspace it needs. */
+int iron_gemm_splitk_choose(int M, int N, int K);
+long long iron_gemm_splitk_workspace_bytes(int M, int N, int splits);
+int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, int M, int N, int K, long long ldc, int epilogue,
+                             int has_clamp, float clamp_lo, float clamp_hi, int splits, void* workspace,
+                             long long workspace_bytes, void* stream);
+
 /* out (cols, rows) = in (rows, cols)^T, bf16. Layout glue for GEMM's
  * row-major B (the role of iron/operators/transpose/op.py:18-120). */
 int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream);

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, list] = {
     "iron_gqa_decode": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P],
     "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
     "iron_gemm_bf16_nt": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _P],
+    "iron_gemm_bf16_nt_splitk": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _I, _P, _LL, _P],
     "iron_transpose_bf16": [_P, _P, _I, _I, _P],
     "iron_transpose_batched_bf16": [_P, _P, _I, _I, _I, _P],
     "iron_repeat_rows": [_P, _P, _LL, _LL, _I, _P],
@@ -56,6 +57,8 @@ SIGNATURES: dict[str, list] = {
 # ... except these queries, which return a value.
 QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
+    "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
+    "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
 }
 
 _lock = threading.Lock()

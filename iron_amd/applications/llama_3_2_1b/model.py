@@ -37,6 +37,7 @@ from dataclasses import dataclass, field
 import torch
 
 from ... import _lib
+from ...common.graph import capture_graph
 
 BF16 = torch.bfloat16
 
@@ -166,10 +167,19 @@ class Linear:
                       x.data_ptr(), y.data_ptr(), self.N, self.K, mode, None, float(eps), _lib.ptr(residual), 0,
                       _lib.ptr(keys), stream)
 
-    def gemm(self, X, Y, rows, stream):
-        """Y (rows, N) = X (rows, K) . W^T on bf16 MFMA."""
-        _lib.call("iron_gemm_bf16_nt", X.data_ptr(), self.bf16.data_ptr(), Y.data_ptr(), rows, self.N, self.K,
-                  self.N, 0, 0, 0.0, 0.0, stream)
+    def gemm(self, X, Y, rows, stream, workspace=None):
+        """Y (rows, N) = X (rows, K) . W^T on bf16 MFMA; split over K (fp32
+        partials in ``workspace(nbytes)``) when the output tiles alone cannot
+        fill the GPU."""
+        splits = _lib.query("iron_gemm_splitk_choose", rows, self.N, self.K) if workspace is not None else 1
+        if splits > 1:
+            need = int(_lib.query("iron_gemm_splitk_workspace_bytes", rows, self.N, splits))
+            ws = workspace(need)
+            _lib.call("iron_gemm_bf16_nt_splitk", X.data_ptr(), self.bf16.data_ptr(), Y.data_ptr(), rows, self.N,
+                      self.K, self.N, 0, 0, 0.0, 0.0, splits, ws.data_ptr(), need, stream)
+        else:
+            _lib.call("iron_gemm_bf16_nt", X.data_ptr(), self.bf16.data_ptr(), Y.data_ptr(), rows, self.N, self.K,
+                      self.N, 0, 0, 0.0, 0.0, stream)
 
 
 class LlamaHIP:
@@ -229,6 +239,7 @@ class LlamaHIP:
         self.host_pos = 0
         self.graph = None
         self._prefill_bufs = {}
+        self._gemm_ws = torch.empty(0, dtype=torch.uint8, device=dev)
         torch.cuda.synchronize(dev)
 
     # ------------------------------------------------------------ helpers
@@ -315,15 +326,7 @@ class LlamaHIP:
     def capture_decode_graph(self) -> None:
         """Capture decode_step() once as a HIP graph (replayed per token)."""
         self._warmup()
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                self.decode_step()
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        self.graph = g
+        self.graph = capture_graph(self.decode_step, self.device)
 
     def decode(self, n_steps: int, use_graph: bool = True) -> None:
         """Run n_steps greedy decode steps from the current token and position."""
@@ -340,6 +343,12 @@ class LlamaHIP:
         self.host_pos += n_steps
 
     # ------------------------------------------------------------ prefill
+    def _workspace(self, nbytes: int) -> torch.Tensor:
+        """Split-K GEMM workspace of at least ``nbytes`` (grown on demand; stream-ordered reuse)."""
+        if self._gemm_ws.numel() < nbytes:
+            self._gemm_ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._gemm_ws
+
     def _pbufs(self, S: int):
         b = self._prefill_bufs.get(S)
         if b is None:
@@ -383,20 +392,20 @@ class LlamaHIP:
             else:  # X += T (previous FFN output), Xn = norm(X)
                 _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
                           float(cfg.eps), s)
-            L["qkv"].gemm(Xn, b["QKV"], S, s)
+            L["qkv"].gemm(Xn, b["QKV"], S, s, self._workspace)
             _lib.call("iron_qkv_rope_scatter", b["QKV"].data_ptr(), self.angles.data_ptr(), self.angles.shape[0],
                       b["Q"].data_ptr(), self.k_cache[i].data_ptr(), self.v_cache[i].data_ptr(), S, cfg.n_heads,
                       cfg.n_kv_groups, Hd, cfg.max_seq_len, pos0, s)
             _lib.call("iron_attention_prefill", b["Q"].data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), b["O"].data_ptr(), cfg.n_heads, cfg.n_kv_groups, S, pos0 + S, Hd,
                       Hd, cfg.n_heads * Hd, cfg.max_seq_len * Hd, Hd, Hd, cfg.n_heads * Hd, S, 1, pos0, scale, s)
-            L["o"].gemm(b["O"], T, S, s)
+            L["o"].gemm(b["O"], T, S, s, self._workspace)
             _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
                       float(cfg.eps), s)
-            L["gate"].gemm(Xn, b["G"], S, s)
-            L["up"].gemm(Xn, b["U"], S, s)
+            L["gate"].gemm(Xn, b["G"], S, s, self._workspace)
+            L["up"].gemm(Xn, b["U"], S, s, self._workspace)
             _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(), S * cfg.hidden_dim, s)
-            L["down"].gemm(b["G"], T, S, s)
+            L["down"].gemm(b["G"], T, S, s, self._workspace)
         _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
                   float(cfg.eps), s)
         self.head.gemv(Xn[S - 1], self.logits, s, keys=self.keys)

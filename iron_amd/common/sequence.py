@@ -52,6 +52,7 @@ from dataclasses import dataclass
 import torch
 
 from .base import AIEOperatorBase, AIERuntimeArgSpec
+from .graph import capture_graph
 
 logger = logging.getLogger(__name__)
 
@@ -562,16 +563,7 @@ class SequenceGraphCallable(SequenceEagerCallable):
     def _capture(self):
         # one eager run first: operators allocate their own scratch on first use
         SequenceEagerCallable._run(self)
-        torch.cuda.synchronize(self.device)
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream(self.device)
-        side.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
-                SequenceEagerCallable._run(self)
-        torch.cuda.current_stream(self.device).wait_stream(side)
-        torch.cuda.synchronize(self.device)
-        self._graph = graph
+        self._graph = capture_graph(lambda: SequenceEagerCallable._run(self), self.device)
 
     def _run(self):
         if self._graph is None:

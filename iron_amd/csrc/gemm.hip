@@ -10,10 +10,12 @@
 //
 // Tiling: 128x128 output tile per 256-thread workgroup, 4 waves in 2x2, each
 // wave owns 64x64 = 2x2 MFMA tiles (64 fp32 accumulators per lane). K advances
-// 64 per step through a double-buffered LDS ring (one barrier per step); the
-// next step's global loads are in flight while MFMAs run. LDS rows are 128 B
-// (64 bf16); the 16-byte chunk c of row r lives at c ^ (r & 7), so the 32 rows
-// read by one fragment load spread over all banks.
+// 64 per step through a double-buffered LDS ring (one barrier per step).
+// Global loads run two steps ahead through two register stages: with one
+// workgroup per CU (the prefill shapes) a single step of look-ahead leaves the
+// MFMAs waiting on L2 latency. LDS rows are 128 B (64 bf16); the 16-byte chunk
+// c of row r lives at c ^ (r & 7), so the 32 rows read by one fragment load
+// spread over all banks.
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive
 // tiles along M (which share one B column block) go to the same XCD, so a
 // weight block is fetched from HBM into one L2 only.
@@ -41,46 +43,84 @@ struct GemmArgs {
   int epi;
   int clamp;
   float lo, hi;
+  float* partial;  // split-K: fp32 (splits, M, N) partial sums instead of C
+  int splits;      // K ranges (1 = no split)
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ (row & 7)); }
 
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+
+// One step's global loads into register stage r (4 A + 4 B chunks per
+// thread). GUARD zero-fills rows past M / N; steps past the end reload the
+// last step (never stored).
+#define IRON_GEMM_LOAD_CHUNK(r, i, k0)                                                                   \
+  {                                                                                                      \
+    const int id_ = tid + (i) * kThreads, row_ = id_ >> 3, c_ = id_ & 7;                                 \
+    const int gm_ = m0 + row_, gn_ = n0 + row_;                                                          \
+    r[i] = (!GUARD || gm_ < a.M) ? *reinterpret_cast<const u32x4v*>(Ag + static_cast<size_t>(gm_) * a.K +   \
+                                                                     (k0) + c_ * 8)                       \
+                                 : u32x4v{0, 0, 0, 0};                                                   \
+    r[4 + (i)] = (!GUARD || gn_ < a.N) ? *reinterpret_cast<const u32x4v*>(Bg + static_cast<size_t>(gn_) *  \
+                                                                          a.K + (k0) + c_ * 8)           \
+                                       : u32x4v{0, 0, 0, 0};                                             \
+  }
+#define IRON_GEMM_LOAD(r, step)                                                                          \
+  {                                                                                                      \
+    const int k0_ = min(step, nk - 1) * BK;                                                              \
+    IRON_GEMM_LOAD_CHUNK(r, 0, k0_) IRON_GEMM_LOAD_CHUNK(r, 1, k0_)                                      \
+    IRON_GEMM_LOAD_CHUNK(r, 2, k0_) IRON_GEMM_LOAD_CHUNK(r, 3, k0_)                                      \
+  }
+#define IRON_GEMM_STORE_CHUNK(r, i, As_, Bs_)                                                            \
+  {                                                                                                      \
+    const int id_ = tid + (i) * kThreads, row_ = id_ >> 3, c_ = id_ & 7;                                 \
+    As_[swz(row_, c_)] = r[i];                                                                           \
+    Bs_[swz(row_, c_)] = r[4 + (i)];                                                                     \
+  }
+#define IRON_GEMM_STORE(r, buf)                                                                          \
+  {                                                                                                      \
+    u32x4v* As_ = reinterpret_cast<u32x4v*>(smem + (buf) * 2 * BM * kChunks);                            \
+    u32x4v* Bs_ = As_ + BM * kChunks;                                                                    \
+    IRON_GEMM_STORE_CHUNK(r, 0, As_, Bs_) IRON_GEMM_STORE_CHUNK(r, 1, As_, Bs_)                          \
+    IRON_GEMM_STORE_CHUNK(r, 2, As_, Bs_) IRON_GEMM_STORE_CHUNK(r, 3, As_, Bs_)                          \
+  }
+// 4 k-slices of 16: per slice each wave reads 2 A and 2 B fragments (one
+// 16-byte LDS read each) and issues its 2x2 MFMAs.
+#define IRON_GEMM_COMPUTE(buf)                                                                           \
+  {                                                                                                      \
+    const uint4* As_ = smem + (buf) * 2 * BM * kChunks;                                                  \
+    const uint4* Bs_ = As_ + BM * kChunks;                                                               \
+    _Pragma("unroll") for (int kk = 0; kk < BK / 16; ++kk) {                                             \
+      const int c_ = kk * 2 + (lane >> 5);                                                               \
+      bf16x8_t fa[2], fb[2];                                                                             \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                                    \
+        fa[i] = __builtin_bit_cast(bf16x8_t, As_[swz(wm * 64 + i * 32 + (lane & 31), c_)]);              \
+        fb[i] = __builtin_bit_cast(bf16x8_t, Bs_[swz(wn * 64 + i * 32 + (lane & 31), c_)]);              \
+      }                                                                                                  \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                      \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                      \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);           \
+    }                                                                                                    \
+  }
+
+template <bool GUARD>
 __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
   __shared__ uint4 smem[2 * 2 * BM * kChunks];  // [buf][A|B][row][chunk] = 64 KiB
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // XCD-aware tile order
+  // XCD-aware tile order (over tiles x K ranges)
   const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
-  const int T = tiles_m * tiles_n;
+  const int T = tiles_m * tiles_n * a.splits;
   int t = blockIdx.x;
   if (T % 8 == 0) t = (t % 8) * (T / 8) + t / 8;
+  const int kb = t / (tiles_m * tiles_n);
+  t %= tiles_m * tiles_n;
   const int tm = t % tiles_m, tn = t / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
-
-  // global -> register staging: 4 A chunks + 4 B chunks per thread per step
-  uint4 ra[4], rb[4];
-  auto load_step = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + i * kThreads, row = id >> 3, c = id & 7;
-      const int gm = m0 + row, gn = n0 + row;
-      ra[i] = gm < a.M ? *reinterpret_cast<const uint4*>(a.A + static_cast<size_t>(gm) * a.K + k0 + c * 8)
-                       : make_uint4(0, 0, 0, 0);
-      rb[i] = gn < a.N ? *reinterpret_cast<const uint4*>(a.B + static_cast<size_t>(gn) * a.K + k0 + c * 8)
-                       : make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_step = [&](int buf) {
-    uint4* As = smem + buf * 2 * BM * kChunks;
-    uint4* Bs = As + BM * kChunks;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + i * kThreads, row = id >> 3, c = id & 7;
-      As[swz(row, c)] = ra[i];
-      Bs[swz(row, c)] = rb[i];
-    }
-  };
+  const int nk = a.K / BK / a.splits;  // steps in this workgroup's K range
+  const uint16_t* Ag = a.A + static_cast<size_t>(kb) * nk * BK;
+  const uint16_t* Bg = a.B + static_cast<size_t>(kb) * nk * BK;
 
   f32x16_t acc[2][2];
 #pragma unroll
@@ -90,33 +130,38 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const int nk = a.K / BK;
-  load_step(0);
-  store_step(0);
+  // two register stages: steps s+1 and s+2 are in flight while step s computes
+  u32x4v st0[8], st1[8];
+  IRON_GEMM_LOAD(st0, 0);
+  IRON_GEMM_LOAD(st1, 1);
+  IRON_GEMM_STORE(st0, 0);
   __syncthreads();
-  for (int it = 0; it < nk; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < nk) load_step((it + 1) * BK);
-    const uint4* As = smem + buf * 2 * BM * kChunks;
-    const uint4* Bs = As + BM * kChunks;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int c = kk * 2 + (lane >> 5);
-      bf16x8_t fa[2], fb[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int ra_row = wm * 64 + i * 32 + (lane & 31);
-        fa[i] = __builtin_bit_cast(bf16x8_t, As[swz(ra_row, c)]);
-        const int rb_row = wn * 64 + i * 32 + (lane & 31);
-        fb[i] = __builtin_bit_cast(bf16x8_t, Bs[swz(rb_row, c)]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-    if (it + 1 < nk) store_step(buf ^ 1);
+  for (int it = 0; it < nk; it += 2) {
+    IRON_GEMM_LOAD(st0, it + 2);
+    IRON_GEMM_COMPUTE(0);  // step it
+    if (it + 1 < nk) IRON_GEMM_STORE(st1, 1);
     __syncthreads();
+    if (it + 1 < nk) {
+      IRON_GEMM_LOAD(st1, it + 3);
+      IRON_GEMM_COMPUTE(1);  // step it + 1
+      if (it + 2 < nk) IRON_GEMM_STORE(st0, 0);
+      __syncthreads();
+    }
+  }
+
+  if (a.partial) {  // split-K: raw fp32 sums straight from the accumulators
+    float* P = a.partial + static_cast<size_t>(kb) * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int gm = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const int gn = n0 + wn * 64 + j * 32 + (lane & 31);
+          if (!GUARD || (gm < a.M && gn < a.N)) P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
+        }
+    return;
   }
 
   // epilogue through LDS: C tile as bf16 [128][128] (32 KiB)
@@ -156,6 +201,29 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
   }
 }
 
+#undef IRON_GEMM_LOAD_CHUNK
+#undef IRON_GEMM_LOAD
+#undef IRON_GEMM_STORE_CHUNK
+#undef IRON_GEMM_STORE
+#undef IRON_GEMM_COMPUTE
+
+// Split-K merge: C = clamp(act(bf16(sum_kb partial[kb]))), the same epilogue
+// order as the single-pass kernel. One thread per output element.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs a) {
+  const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  const long long mn = static_cast<long long>(a.M) * a.N;
+  if (t >= mn) return;
+  float x = 0.f;
+  for (int kb = 0; kb < a.splits; ++kb) x += a.partial[kb * mn + t];
+  if (a.epi != EPI_NONE || a.clamp) {
+    x = bf16_to_f32(f32_to_bf16(x));
+    x = apply_epilogue(x, a.epi);
+    if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
+  }
+  const long long m = t / a.N, n = t % a.N;
+  a.C[m * a.ldc + n] = f32_to_bf16(x);
+}
+
 // 64x64 tiled transpose through LDS: out (cols, rows) = in (rows, cols)^T.
 __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                                         int rows, int cols) {
@@ -177,23 +245,78 @@ __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restri
 
 using namespace iron;
 
+static int gemm_check(const char* fn, const void* A, const void* B, const void* C, int M, int N, int K,
+                      long long ldc, int epilogue, int has_clamp, float clamp_lo, float clamp_hi) {
+  IRON_REQUIRE(A && B && C, "%s: null pointer", fn);
+  IRON_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d must be positive", fn, M, N, K);
+  IRON_REQUIRE(K % BK == 0, "%s: K=%d must be a multiple of %d", fn, K, BK);
+  IRON_REQUIRE(aligned16(A) && aligned16(B), "%s: A and B must be 16-byte aligned", fn);
+  IRON_REQUIRE(ldc >= N, "%s: ldc=%lld < N=%d", fn, ldc, N);
+  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "%s: bad epilogue %d", fn, epilogue);
+  IRON_REQUIRE(!has_clamp || clamp_lo <= clamp_hi, "%s: clamp min > max", fn);
+  if ((ldc % 8 == 0) && !aligned16(C)) return fail_einval("%s: C must be 16-byte aligned", fn);
+  return 0;
+}
+
+static void gemm_launch(const GemmArgs& a, hipStream_t s) {
+  const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * a.splits;
+  if (a.M % BM == 0 && a.N % BN == 0)
+    IRON_LAUNCH(gemm_nt_kernel<false>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, s, a);
+  else
+    IRON_LAUNCH(gemm_nt_kernel<true>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, s, a);
+}
+
 extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K, long long ldc,
                                  int epilogue, int has_clamp, float clamp_lo, float clamp_hi, void* stream) {
-  IRON_REQUIRE(A && B && C, "iron_gemm_bf16_nt: null pointer");
-  IRON_REQUIRE(M > 0 && N > 0 && K > 0, "iron_gemm_bf16_nt: M=%d N=%d K=%d must be positive", M, N, K);
-  IRON_REQUIRE(K % BK == 0, "iron_gemm_bf16_nt: K=%d must be a multiple of %d", K, BK);
-  IRON_REQUIRE(aligned16(A) && aligned16(B), "iron_gemm_bf16_nt: A and B must be 16-byte aligned");
-  IRON_REQUIRE(ldc >= N, "iron_gemm_bf16_nt: ldc=%lld < N=%d", ldc, N);
-  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemm_bf16_nt: bad epilogue %d", epilogue);
-  IRON_REQUIRE(!has_clamp || clamp_lo <= clamp_hi, "iron_gemm_bf16_nt: clamp min > max");
-  if ((ldc % 8 == 0) && !aligned16(C)) return fail_einval("iron_gemm_bf16_nt: C must be 16-byte aligned");
-  GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
-             ldc, epilogue, has_clamp, clamp_lo, clamp_hi};
+  if (int rc = gemm_check("iron_gemm_bf16_nt", A, B, C, M, N, K, ldc, epilogue, has_clamp, clamp_lo, clamp_hi))
+    return rc;
   const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt: problem too large");
-  IRON_LAUNCH(gemm_nt_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
+             ldc, epilogue, has_clamp, clamp_lo, clamp_hi, nullptr, 1};
+  gemm_launch(a, static_cast<hipStream_t>(stream));
   return check_launch("gemm_bf16_nt");
+}
+
+extern "C" int iron_gemm_splitk_choose(int M, int N, int K) {
+  // Split K while the workgroups stay within 1.25x the 256 CUs and every K range
+  // keeps >= 8 steps of 64; at most 8 ranges.
+  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 1;
+  const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  int s = 1;
+  while (s < 8 && tiles * s * 2 <= 320 && (K / BK) % (s * 2) == 0 && K / BK / (s * 2) >= 8) s *= 2;
+  return s;
+}
+
+extern "C" long long iron_gemm_splitk_workspace_bytes(int M, int N, int splits) {
+  if (M <= 0 || N <= 0 || splits <= 0) return -1;
+  return splits > 1 ? static_cast<long long>(splits) * M * N * 4 : 0;
+}
+
+extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, int M, int N, int K, long long ldc,
+                                        int epilogue, int has_clamp, float clamp_lo, float clamp_hi, int splits,
+                                        void* workspace, long long workspace_bytes, void* stream) {
+  if (int rc = gemm_check("iron_gemm_bf16_nt_splitk", A, B, C, M, N, K, ldc, epilogue, has_clamp, clamp_lo,
+                          clamp_hi))
+    return rc;
+  IRON_REQUIRE(splits >= 1 && (K / BK) % splits == 0,
+               "iron_gemm_bf16_nt_splitk: splits=%d must divide the %d K steps of 64", splits, K / BK);
+  if (splits == 1)
+    return iron_gemm_bf16_nt(A, B, C, M, N, K, ldc, epilogue, has_clamp, clamp_lo, clamp_hi, stream);
+  const long long need = static_cast<long long>(splits) * M * N * 4;
+  IRON_REQUIRE(workspace && workspace_bytes >= need, "iron_gemm_bf16_nt_splitk: workspace of %lld bytes < %lld",
+               workspace_bytes, need);
+  IRON_REQUIRE(aligned16(workspace), "iron_gemm_bf16_nt_splitk: workspace must be 16-byte aligned");
+  const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN) * splits;
+  IRON_REQUIRE(tiles < (1LL << 31) && static_cast<long long>(M) * N < (1LL << 38),
+               "iron_gemm_bf16_nt_splitk: problem too large");
+  GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
+             ldc, epilogue, has_clamp, clamp_lo, clamp_hi, static_cast<float*>(workspace), splits};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  gemm_launch(a, s);
+  const long long mn = static_cast<long long>(M) * N;
+  IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
+  return check_launch("gemm_bf16_nt_splitk");
 }
 
 extern "C" int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream) {

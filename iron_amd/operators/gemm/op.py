@@ -6,7 +6,9 @@ The AIE tiling knobs are accepted and ignored. K must be a multiple of 64.
 
 Kernel: iron_gemm_bf16_nt (A and B both K-contiguous). B given row-major
 (K, N) is first transposed into an operator-owned scratch buffer; a
-column-major C is produced by computing C^T = B A^T.
+column-major C is produced by computing C^T = B A^T. Shapes whose output
+tiles cannot fill the GPU are split over K (iron_gemm_bf16_nt_splitk, fp32
+partials in an operator-owned workspace).
 """
 
 from dataclasses import dataclass, field
@@ -57,6 +59,7 @@ class GEMM(HIPOperator):
         if self.dtype_in not in _DTYPES or self.dtype_out not in _DTYPES:
             raise ValueError(f"only bf16 in/out is supported (got {self.dtype_in}/{self.dtype_out})")
         self._bt = {}
+        self._ws = {}
         HIPOperator.__init__(self, context=self.context)
 
     def get_arg_spec(self):
@@ -77,11 +80,25 @@ class GEMM(HIPOperator):
         _lib.call("iron_transpose_bf16", B.data_ptr(), bt.data_ptr(), self.K, self.N, stream)
         return bt
 
+    def _nt(self, X, W, C, rows, cols, stream):
+        """C (rows, cols) = X (rows, K) . W (cols, K)^T, split over K when the
+        output tiles alone cannot fill the GPU (operator-owned workspace)."""
+        splits = _lib.query("iron_gemm_splitk_choose", rows, cols, self.K)
+        if splits > 1:
+            need = int(_lib.query("iron_gemm_splitk_workspace_bytes", rows, cols, splits))
+            ws = self._ws.get(X.device)
+            if ws is None or ws.numel() < need:
+                ws = torch.empty(need, dtype=torch.uint8, device=X.device)
+                self._ws[X.device] = ws
+            _lib.call("iron_gemm_bf16_nt_splitk", X.data_ptr(), W.data_ptr(), C.data_ptr(), rows, cols, self.K,
+                      cols, 0, 0, 0.0, 0.0, splits, ws.data_ptr(), need, stream)
+        else:
+            _lib.call("iron_gemm_bf16_nt", X.data_ptr(), W.data_ptr(), C.data_ptr(), rows, cols, self.K, cols, 0, 0,
+                      0.0, 0.0, stream)
+
     def _launch(self, A, B, C, *, stream):
         Bnk = self._b_nk(B, stream)
         if self.c_col_maj:
-            _lib.call("iron_gemm_bf16_nt", Bnk.data_ptr(), A.data_ptr(), C.data_ptr(), self.N, self.M, self.K,
-                      self.M, 0, 0, 0.0, 0.0, stream)
+            self._nt(Bnk, A, C, self.N, self.M, stream)
         else:
-            _lib.call("iron_gemm_bf16_nt", A.data_ptr(), Bnk.data_ptr(), C.data_ptr(), self.M, self.N, self.K,
-                      self.N, 0, 0, 0.0, 0.0, stream)
+            self._nt(A, Bnk, C, self.M, self.N, stream)

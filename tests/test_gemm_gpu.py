@@ -97,3 +97,51 @@ def test_prefill_gemm_shapes(gpu, M, K, N):
     assert rel_l2 <= 1e-2
     bad = ops.within_bf16_ulps(C, ref, n_ulp=1.0, atol=1e-5 * float(ref.abs().max()))
     assert not bad, bad[:5]
+
+
+@pytest.mark.parametrize("M,K,N,splits", [(512, 8192, 2048, 4), (512, 2048, 2048, 4), (512, 2048, 3072, 2),
+                                          (100, 512, 200, 2), (256, 1024, 384, 8), (64, 4096, 64, 8)])
+@pytest.mark.parametrize("epi,clamp", [(0, False), (2, False), (4, True)])
+def test_gemm_splitk(gpu, M, K, N, splits, epi, clamp):
+    """Split-K GEMM (fp32 partials + ordered merge) against the fp32 reference
+    with the flm epilogue order (round to bf16, activation, clamp), and (with
+    no epilogue) against the single-pass kernel: within one bf16 ulp of it."""
+    from iron_amd import _lib
+
+    g = torch.Generator().manual_seed(M + K + N + splits)
+    A = (torch.randn(M, K, generator=g) * 0.5).to(BF16)
+    W = (torch.randn(N, K, generator=g) * 0.5).to(BF16)
+    s = _lib.stream_handle(gpu)
+    Ad, Wd = A.to(gpu), W.to(gpu)
+    C1 = torch.empty(M, N, dtype=BF16, device=gpu)
+    C2 = torch.empty(M, N, dtype=BF16, device=gpu)
+    lo, hi = (-1.5, 2.0) if clamp else (0.0, 0.0)
+    need = int(_lib.query("iron_gemm_splitk_workspace_bytes", M, N, splits))
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    _lib.call("iron_gemm_bf16_nt_splitk", Ad.data_ptr(), Wd.data_ptr(), C1.data_ptr(), M, N, K, N, epi, int(clamp),
+              lo, hi, splits, ws.data_ptr(), need, s)
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), C2.data_ptr(), M, N, K, N, epi, int(clamp), lo, hi, s)
+    torch.cuda.synchronize()
+    names = {0: "none", 2: "silu", 4: "gelu"}
+    ref = ops.flm_apply_epilogue((A.float() @ W.float().T).to(BF16), names[epi], (lo, hi) if clamp else None)
+    mass = (A.float().abs() @ W.float().abs().T)
+    err = (C1.cpu().float() - ref.float()).abs()
+    assert torch.all(err <= 2.0**-7 * ref.float().abs() + 2.0**-12 * mass + 1e-3), float(err.max())
+    if epi == 0 and not clamp:  # an activation can stretch a 1-ulp input flip past one output ulp
+        assert not ops.within_bf16_ulps(C1.cpu(), C2.cpu().float(), n_ulp=1.0, atol=2.0**-14 * float(mass.max()))
+
+
+def test_gemm_splitk_choice_and_errors(gpu):
+    from iron_amd import _lib
+
+    assert _lib.query("iron_gemm_splitk_choose", 512, 2048, 8192) == 4
+    assert _lib.query("iron_gemm_splitk_choose", 512, 8192, 2048) == 1  # 256 tiles already fill the GPU
+    assert _lib.query("iron_gemm_splitk_choose", 4096, 4096, 4096) == 1
+    A = torch.zeros(128, 192, dtype=BF16, device=gpu)
+    C = torch.zeros(128, 128, dtype=BF16, device=gpu)
+    with pytest.raises(_lib.IronHipError, match="must divide"):
+        _lib.call("iron_gemm_bf16_nt_splitk", A.data_ptr(), A.data_ptr(), C.data_ptr(), 128, 128, 192, 128, 0, 0,
+                  0.0, 0.0, 2, C.data_ptr(), C.numel() * 2, _lib.stream_handle(gpu))
+    with pytest.raises(_lib.IronHipError, match="workspace"):
+        _lib.call("iron_gemm_bf16_nt_splitk", A.data_ptr(), A.data_ptr(), C.data_ptr(), 128, 128, 192, 128, 0, 0,
+                  0.0, 0.0, 3, C.data_ptr(), 16, _lib.stream_handle(gpu))
