@@ -291,10 +291,20 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 }
 
 // ---------------------------------------------------------------------------
-// Prefill / MHA: causal (optional) flash attention over strided Q, K, V.
-// Block = 64 queries of one head, 256 threads: thread -> (query t/4, quarter
-// t%4). K/V tiles of 64 keys are staged in LDS as fp32; the online softmax
-// keeps a running max and sum per query (log2 domain).
+// Prefill / MHA: causal (optional) flash attention over strided Q, K, V on
+// MFMA (v_mfma_f32_32x32x16_bf16).
+//
+// Workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries and
+// walks the visible keys in blocks of 64 staged in LDS (K row-major with the
+// 16-byte chunk XOR swizzle, V transposed to [dim][key]). Per block a wave
+// computes S^T = K Q^T (two 32x32 tiles): every lane then holds one query
+// column (lane % 32) and 16 keys, so the softmax row statistics need only the
+// lane's own registers and one exchange with lane ^ 32. The probabilities go
+// to bf16 and feed O^T += V^T P^T directly from registers as the B operand;
+// the k index of that product is a permutation of the block's keys that
+// matches the S^T accumulator layout, and V^T is read in the same order.
+// Online softmax in the log2 domain, fp32 statistics; output rows in
+// [Sq, out_rows) are zero-filled (the MHA operator's padding).
 // ---------------------------------------------------------------------------
 struct PrefillArgs {
   const uint16_t* q;
@@ -312,122 +322,162 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-constexpr int kPfQ = 64, kPfK = 64;
+typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int fa_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int fa_u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kFaQ = 128;      // queries per workgroup (4 waves x 32)
+constexpr int kFaK = 64;       // keys per block
+constexpr int kVtStride = 68;  // V^T row: 64 keys + 4 pad (136 B: 8-byte reads of 32 rows hit distinct banks)
+constexpr int kOutStride = 72; // output staging row (144 B)
+constexpr int kFaLds = (kFaK * 128 + kD * kVtStride * 2) > (4 * 32 * kOutStride * 2)
+                           ? (kFaK * 128 + kD * kVtStride * 2)
+                           : (4 * 32 * kOutStride * 2);
 
 __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
-  __shared__ float k_s[kPfK][kD + 1];
-  __shared__ float v_s[kPfK][kD];
-  __shared__ float p_s[kPfQ][kPfK + 1];
-  const int tid = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kFaLds];
+  fa_u32x4* k_s = reinterpret_cast<fa_u32x4*>(lds);                 // [key][chunk ^ (key & 7)]
+  uint16_t* vt_s = reinterpret_cast<uint16_t*>(lds + kFaK * 128);   // [dim][key]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 31, hh = lane >> 5;
   const int h = blockIdx.y, hk = h / (a.H / a.Hkv);
-  const int q0 = blockIdx.x * kPfQ;
-  const int qi = tid >> 2, sub = tid & 3;
-  const int qrow = q0 + qi;
-  const bool qvalid = qrow < a.Sq;
-  const int qpos = a.q_offset + qrow;
-  if (q0 >= a.Sq) {  // padding rows only (uniform per block)
-    if (qrow < a.out_rows) {
-      uint16_t* op = a.out + h * a.o_hs + static_cast<long long>(qrow) * a.o_rs + sub * 16;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) op[i] = 0;
+  const int q0 = blockIdx.x * kFaQ;
+  if (q0 >= a.Sq) {  // padding rows only (uniform per workgroup)
+    for (int e = tid; e < kFaQ * (kD / 8); e += 256) {
+      const int r = q0 + (e >> 3), ch = e & 7;
+      if (r < a.out_rows)
+        *reinterpret_cast<fa_u32x4*>(a.out + h * a.o_hs + static_cast<long long>(r) * a.o_rs + ch * 8) =
+            fa_u32x4{0, 0, 0, 0};
     }
     return;
   }
+  const int qw = q0 + wave * 32;  // this wave's first query row
 
-  float qv[kD];
+  // Q fragments (B operand of S^T): query qw + c, dims 16 kk + 8 hh .. + 8
+  fa_bf16x8 qf[4];
   {
-    const uint16_t* qp = a.q + h * a.q_hs + static_cast<long long>(qvalid ? qrow : 0) * a.q_rs;
+    const int qrow = min(qw + c, a.Sq - 1);
+    const uint16_t* qp = a.q + h * a.q_hs + static_cast<long long>(qrow) * a.q_rs;
 #pragma unroll
-    for (int d = 0; d < kD; d += 8) {
-      const uint4 t = *reinterpret_cast<const uint4*>(qp + d);
-      const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qv[d + 2 * e] = lo_bf16(w[e]) * a.scale_log2;
-        qv[d + 2 * e + 1] = hi_bf16(w[e]) * a.scale_log2;
-      }
-    }
+    for (int kk = 0; kk < 4; ++kk)
+      qf[kk] = __builtin_bit_cast(fa_bf16x8, *reinterpret_cast<const fa_u32x4*>(qp + 16 * kk + 8 * hh));
   }
-  float o[16];
+  fa_f32x16 o[2];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) o[i] = 0.f;
+  for (int j = 0; j < 16; ++j) o[0][j] = o[1][j] = 0.f;
   float m = -INFINITY, l = 0.f;
-
-  // keys visible to the block: up to the last query's position (causal)
+  const int qpos = a.q_offset + qw + c;  // absolute position of this lane's query
   int kend = a.Skv;
-  if (a.causal) {
-    const int last = a.q_offset + min(q0 + kPfQ, a.Sq) - 1;
-    kend = min(kend, last + 1);
-  }
-  for (int k0 = 0; k0 < kend; k0 += kPfK) {
-    __syncthreads();
-    for (int e = tid; e < kPfK * (kD / 8); e += 256) {
-      const int kr = e / (kD / 8), dc = (e % (kD / 8)) * 8;
-      const int key = k0 + kr;
-      uint4 kt = make_uint4(0, 0, 0, 0), vt = make_uint4(0, 0, 0, 0);
+  if (a.causal) kend = min(kend, a.q_offset + min(q0 + kFaQ, a.Sq));
+  const int wave_last = a.q_offset + min(qw + 31, a.Sq - 1);
+
+  for (int k0 = 0; k0 < kend; k0 += kFaK) {
+    __syncthreads();  // the previous block's LDS reads are done
+    for (int e = tid; e < kFaK * 8; e += 256) {
+      const int kr = e >> 3, ch = e & 7, key = k0 + kr;
+      fa_u32x4 kt = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
       if (key < a.Skv) {
-        kt = *reinterpret_cast<const uint4*>(a.k + hk * a.k_hs + static_cast<long long>(key) * a.k_rs + dc);
-        vt = *reinterpret_cast<const uint4*>(a.v + hk * a.v_hs + static_cast<long long>(key) * a.v_rs + dc);
+        kt = *reinterpret_cast<const fa_u32x4*>(a.k + hk * a.k_hs + static_cast<long long>(key) * a.k_rs + ch * 8);
+        vv = *reinterpret_cast<const fa_u32x4*>(a.v + hk * a.v_hs + static_cast<long long>(key) * a.v_rs + ch * 8);
       }
-      const uint32_t kw[4] = {kt.x, kt.y, kt.z, kt.w}, vw[4] = {vt.x, vt.y, vt.z, vt.w};
+      k_s[kr * 8 + (ch ^ (kr & 7))] = kt;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        k_s[kr][dc + 2 * q] = lo_bf16(kw[q]);
-        k_s[kr][dc + 2 * q + 1] = hi_bf16(kw[q]);
-        v_s[kr][dc + 2 * q] = lo_bf16(vw[q]);
-        v_s[kr][dc + 2 * q + 1] = hi_bf16(vw[q]);
+      for (int w = 0; w < 4; ++w) {
+        vt_s[(ch * 8 + 2 * w) * kVtStride + kr] = static_cast<uint16_t>(vv[w] & 0xffffu);
+        vt_s[(ch * 8 + 2 * w + 1) * kVtStride + kr] = static_cast<uint16_t>(vv[w] >> 16);
       }
     }
     __syncthreads();
-    // scores for keys sub*16 .. sub*16+15
-    float sc[16];
-    float tmax = -INFINITY;
+    if (a.causal && k0 > wave_last) continue;  // every key of the block is after this wave's queries
+
+    // S^T = K Q^T: s[b][j] is key k0 + 32 b + 8 (j / 4) + 4 hh + j % 4, query qw + c
+    fa_f32x16 s[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kr = sub * 16 + i, key = k0 + kr;
-      float d = 0.f;
+    for (int b = 0; b < 2; ++b) {
 #pragma unroll
-      for (int e = 0; e < kD; ++e) d = fmaf(qv[e], k_s[kr][e], d);
-      const bool vis = key < a.Skv && (!a.causal || key <= qpos);
-      sc[i] = vis ? d : -INFINITY;
-      tmax = fmaxf(tmax, sc[i]);
+      for (int j = 0; j < 16; ++j) s[b][j] = 0.f;
+      const int kr = 32 * b + c;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const fa_bf16x8 kf = __builtin_bit_cast(fa_bf16x8, k_s[kr * 8 + ((2 * kk + hh) ^ (kr & 7))]);
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[b], 0, 0, 0);
+      }
     }
-    // the 4 threads of a query are lanes 4q..4q+3
-    tmax = fmaxf(tmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                           static_cast<int>(0xff800000u), __builtin_bit_cast(int, tmax), 0xB1, 0xf, 0xf, false)));
-    tmax = fmaxf(tmax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                           static_cast<int>(0xff800000u), __builtin_bit_cast(int, tmax), 0x4E, 0xf, 0xf, false)));
-    const float mnew = fmaxf(m, tmax);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = k0 + 32 * b + 8 * (j >> 2) + 4 * hh + (j & 3);
+        const bool vis = key < a.Skv && (!a.causal || key <= qpos);
+        const float v = vis ? s[b][j] * a.scale_log2 : -INFINITY;
+        s[b][j] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float mnew = fmaxf(m, mx);
     const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m - mnew);
+    // P^T fragments: pf[2 b + sp] element i = register 8 sp + i of s[b]
+    fa_bf16x8 pf[4];
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float p = (sc[i] == -INFINITY) ? 0.f : exp2f(sc[i] - mnew);
-      psum += p;
-      p_s[qi][sub * 16 + i] = p;
-    }
-    psum = add_dpp<0xB1>(psum);
-    psum = add_dpp<0x4E>(psum);
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float x = s[b][8 * sp + i];
+          p[i] = (x == -INFINITY) ? 0.f : exp2f(x - mnew);
+          psum += p[i];
+        }
+        const fa_u32x4 w = {cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
+                            cvt_pk_bf16(p[6], p[7])};
+        pf[2 * b + sp] = __builtin_bit_cast(fa_bf16x8, w);
+      }
     l = l * alpha + psum;
     m = mnew;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] *= alpha;
-    __syncthreads();
-    for (int kr = 0; kr < kPfK; ++kr) {
-      const float p = p_s[qi][kr];
+    for (int j = 0; j < 16; ++j) {
+      o[0][j] *= alpha;
+      o[1][j] *= alpha;
+    }
+    // O^T += V^T P^T over the block's 64 keys, 4 k-steps of 16 in the permuted key order
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[i] = fmaf(p, v_s[kr][sub * 16 + i], o[i]);
+    for (int db = 0; db < 2; ++db) {
+      const uint16_t* vrow = vt_s + (32 * db + c) * kVtStride;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kb = 16 * st + 4 * hh;  // keys kb..kb+3 and kb+8..kb+11 (32 (st / 2) + 16 (st % 2) = 16 st)
+        const fa_u32x2 lo = *reinterpret_cast<const fa_u32x2*>(vrow + kb);
+        const fa_u32x2 hi = *reinterpret_cast<const fa_u32x2*>(vrow + kb + 8);
+        const fa_u32x4 vw = {lo.x, lo.y, hi.x, hi.y};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(fa_bf16x8, vw), pf[st], o[db], 0, 0, 0);
+      }
     }
   }
-  if (qvalid) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = a.out + h * a.o_hs + static_cast<long long>(qrow) * a.o_rs + sub * 16;
+
+  l += __shfl_xor(l, 32, kWave);  // the two halves summed different keys of the same query
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  __syncthreads();  // every wave is done with the K/V tiles
+  uint16_t* stg = reinterpret_cast<uint16_t*>(lds) + wave * 32 * kOutStride;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) op[i] = f32_to_bf16(o[i] * inv);
-  } else if (qrow < a.out_rows) {
-    uint16_t* op = a.out + h * a.o_hs + static_cast<long long>(qrow) * a.o_rs + sub * 16;
+  for (int db = 0; db < 2; ++db)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) op[i] = 0;
+    for (int j = 0; j < 16; ++j) {
+      const int d = 32 * db + 8 * (j >> 2) + 4 * hh + (j & 3);
+      stg[c * kOutStride + d] = f32_to_bf16(o[db][j] * inv);
+    }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i, r = e >> 3, ch = e & 7, q = qw + r;
+    uint16_t* dst = a.out + h * a.o_hs + static_cast<long long>(q) * a.o_rs + ch * 8;
+    if (q < a.Sq)
+      *reinterpret_cast<fa_u32x4*>(dst) = *reinterpret_cast<const fa_u32x4*>(stg + r * kOutStride + ch * 8);
+    else if (q < a.out_rows)
+      *reinterpret_cast<fa_u32x4*>(dst) = fa_u32x4{0, 0, 0, 0};
   }
 }
 
@@ -539,7 +589,9 @@ extern "C" int iron_attention_prefill(const void* q, const void* k, const void* 
                 causal,
                 q_offset,
                 scale * 1.4426950408889634f};
-  dim3 grid((out_rows + kPfQ - 1) / kPfQ, n_heads), block(256);
+  IRON_REQUIRE(aligned16(out) && o_row_stride % 8 == 0 && o_head_stride % 8 == 0,
+               "iron_attention_prefill: out rows must be 16-byte aligned");
+  dim3 grid((out_rows + kFaQ - 1) / kFaQ, n_heads), block(256);
   IRON_LAUNCH(attention_prefill_kernel, grid, block, 0, static_cast<hipStream_t>(stream), a);
   return check_launch("attention_prefill");
 }
