@@ -298,6 +298,31 @@ def bench_prefill_gemm(torch, lib, tm, dev, n):
             "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
+def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
+    """Causal GQA prefill attention of cfg 5's long prompt (32/8 heads, d 64):
+    useful flops 4 * S * (S + 1) / 2 * d per head (QK^T and PV, visible keys)."""
+    from iron_amd import _lib
+
+    H, Hkv, D = 32, 8, 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(S, H * D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    o = torch.empty(S, H * D, dtype=torch.bfloat16, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def launch(i):
+        _check(lib, lib.iron_attention_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), H, Hkv, S, S,
+                                               D, D, H * D, S * D, D, D, H * D, S, 1, 0, 0.125, stream))
+
+    for i in range(5):
+        launch(i)
+    t = tm.kernel_us(launch, n)
+    flops = 4.0 * S * (S + 1) / 2 * D * H
+    tf = flops / t / 1e6
+    return {"seq": S, "kernel_us": round(t, 3), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+
+
 def bench_model(torch, dev, decode_steps=128, prompt_len=512, long_ctx=3968):
     """Config 5: random-init Llama-3.2-1B shape, int4-g32 linears, bf16 tied head."""
     from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
@@ -461,6 +486,7 @@ def main() -> int:
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
             "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200),
             "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+            "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
             "llama_cfg5": bench_model(torch, dev),
         }
         out["extra"] = extra

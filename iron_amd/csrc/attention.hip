@@ -75,14 +75,17 @@ __device__ __forceinline__ void rope_chunk(const uint4 own, const uint4 pair, co
 
 // Partials of one 64-position chunk of KV head j for its G query heads.
 // Thread -> (position rows r and r + 32 of the chunk, dims 8c..8c+7). Every
-// global load the workgroup needs (K/V rows, q and its RoPE partner chunks,
-// the table row, the new k/v) is issued right after `pos` is known, before
-// any barrier, so the kernel pays one memory round trip after the position.
+// global load the workgroup needs (K/V rows, q and its RoPE partner, the
+// table row, the new k/v) is issued right after `pos` is known, before any
+// barrier, so the kernel pays one memory round trip after the position. q is
+// rotated once per workgroup (one element per thread) and shared through LDS;
+// a per-thread rotation of its own chunks would repeat the work 32 times.
 template <int G>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int NW = kDecThreads / kWave;
   constexpr int PS = part_stride<G>();
+  __shared__ __attribute__((aligned(16))) float q_s[G][D];  // rotated q
   __shared__ float max_s[NW][G];
   __shared__ float sum_s[NW][G];
   // per (head, position row, dim); rows padded to 65 floats so the 8x8 (row, chunk) lanes of a
@@ -111,16 +114,19 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
       vraw[h] = ld_stream16(a.v_cache + off);
     }
   }
+  // q rotated once per workgroup: thread t -> element (t / 64, t % 64) into LDS
   const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
-  uint4 qa[G], qb[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    qa[g] = *reinterpret_cast<const uint4*>(qh + g * D + c * 8);
-    qb[g] = *reinterpret_cast<const uint4*>(qh + g * D + (c ^ 4) * 8);
+  const float* angrow = a.angles + static_cast<size_t>(pos) * D;
+  for (int t = tid; t < G * D; t += kDecThreads) {
+    const int d = t % D, i = d & 31;
+    const float x = bf16_to_f32(qh[t]), xp = bf16_to_f32(qh[t ^ 32]);
+    const float cs = angrow[2 * i], sn = angrow[2 * i + 1];
+    q_s[t / D][d] = bf16_to_f32(f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn));
   }
   float ang[16];
-  {
-    const float4* ap = reinterpret_cast<const float4*>(a.angles + static_cast<size_t>(pos) * D + (c & 3) * 16);
+  uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
+  if (owner) {
+    const float4* ap = reinterpret_cast<const float4*>(angrow + (c & 3) * 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 t = ap[i];
@@ -129,17 +135,19 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
       ang[4 * i + 2] = t.z;
       ang[4 * i + 3] = t.w;
     }
-  }
-  uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
-  if (owner) {
     kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + c * 8);
     knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (c ^ 4) * 8);
     vn = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + c * 8);
   }
-
+  __syncthreads();
   float qv[G][8];
 #pragma unroll
-  for (int g = 0; g < G; ++g) rope_chunk(qa[g], qb[g], ang, lower, qv[g]);
+  for (int g = 0; g < G; ++g) {
+    const float4 lo = *reinterpret_cast<const float4*>(&q_s[g][c * 8]);
+    const float4 hi = *reinterpret_cast<const float4*>(&q_s[g][c * 8 + 4]);
+    qv[g][0] = lo.x; qv[g][1] = lo.y; qv[g][2] = lo.z; qv[g][3] = lo.w;
+    qv[g][4] = hi.x; qv[g][5] = hi.y; qv[g][6] = hi.z; qv[g][7] = hi.w;
+  }
   float kf[2][8], vf[2][8];
   bool valid[2];
 #pragma unroll
