@@ -100,6 +100,7 @@ class GEMM(HIPOperator):
                 raise ValueError(f"clamp min ({lo}) must be <= max ({hi})")
         if self.rounding is not Rounding.CONV_EVEN:
             raise ValueError("only round-to-nearest-even conversion is implemented")
+        self._ws = {}
         HIPOperator.__init__(self, context=self.context)
 
     def pack_B(self, B: torch.Tensor) -> torch.Tensor:
@@ -120,5 +121,16 @@ class GEMM(HIPOperator):
 
     def _launch(self, A, B, C, *, stream):
         lo, hi = (float(self.clamp[0]), float(self.clamp[1])) if self.clamp is not None else (0.0, 0.0)
-        _lib.call("iron_gemm_bf16_nt", A.data_ptr(), B.data_ptr(), C.data_ptr(), self.M, self.N, self.K, self.N,
-                  _EPI_CODE[self.epilogue], int(self.clamp is not None), lo, hi, stream)
+        epi, has_clamp = _EPI_CODE[self.epilogue], int(self.clamp is not None)
+        splits = _lib.query("iron_gemm_splitk_choose", self.M, self.N, self.K)
+        if splits > 1:  # output tiles alone cannot fill the GPU: split K, merge applies the epilogue
+            need = int(_lib.query("iron_gemm_splitk_workspace_bytes", self.M, self.N, splits))
+            ws = self._ws.get(A.device)
+            if ws is None or ws.numel() < need:
+                ws = torch.empty(need, dtype=torch.uint8, device=A.device)
+                self._ws[A.device] = ws
+            _lib.call("iron_gemm_bf16_nt_splitk", A.data_ptr(), B.data_ptr(), C.data_ptr(), self.M, self.N, self.K,
+                      self.N, epi, has_clamp, lo, hi, splits, ws.data_ptr(), need, stream)
+        else:
+            _lib.call("iron_gemm_bf16_nt", A.data_ptr(), B.data_ptr(), C.data_ptr(), self.M, self.N, self.K, self.N,
+                      epi, has_clamp, lo, hi, stream)
