@@ -542,8 +542,9 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
       }
       [[fallthrough]];
     case 8192:
-      if (a.K == 8192) {
-        launch_i4_fast<1, 1, 4, PAIR>(a, norm_mode, s);
+      if (a.K == 8192) {  // 4 waves split each row; two rows per workgroup when they fit
+        if (!PAIR && a.M % 2 == 0) launch_i4_fast<1, 2, 4, PAIR>(a, norm_mode, s);
+        else launch_i4_fast<1, 1, 4, PAIR>(a, norm_mode, s);
         break;
       }
       [[fallthrough]];
