@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 //
 // Workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries and
 // walks the visible keys in blocks of 64 staged in LDS (K row-major with the
-// 16-byte chunk XOR swizzle, V transposed to [dim][key]). Per block a wave
+// 16-byte chunk at slot chunk ^ ((key / 2) % 8), which keeps the 16 lanes of
+// a fragment read on distinct banks; V transposed to [dim][key]). Per block a wave
 // computes S^T = K Q^T (two 32x32 tiles): every lane then holds one query
 // column (lane % 32) and 16 keys, so the softmax row statistics need only the
 // lane's own registers and one exchange with lane ^ 32. The probabilities go
@@ -345,7 +346,7 @@ constexpr int kFaLds = (kFaK * 128 + kD * kVtStride * 2) > (4 * 32 * kOutStride 
 
 __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kFaLds];
-  fa_u32x4* k_s = reinterpret_cast<fa_u32x4*>(lds);                 // [key][chunk ^ (key & 7)]
+  fa_u32x4* k_s = reinterpret_cast<fa_u32x4*>(lds);                 // [key][chunk ^ ((key / 2) % 8)]
   uint16_t* vt_s = reinterpret_cast<uint16_t*>(lds + kFaK * 128);   // [dim][key]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 31, hh = lane >> 5;
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
         kt = *reinterpret_cast<const fa_u32x4*>(a.k + hk * a.k_hs + static_cast<long long>(key) * a.k_rs + ch * 8);
         vv = *reinterpret_cast<const fa_u32x4*>(a.v + hk * a.v_hs + static_cast<long long>(key) * a.v_rs + ch * 8);
       }
-      k_s[kr * 8 + (ch ^ (kr & 7))] = kt;
+      k_s[kr * 8 + (ch ^ ((kr >> 1) & 7))] = kt;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         vt_s[(ch * 8 + 2 * w) * kVtStride + kr] = static_cast<uint16_t>(vv[w] & 0xffffu);
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
       const int kr = 32 * b + c;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const fa_bf16x8 kf = __builtin_bit_cast(fa_bf16x8, k_s[kr * 8 + ((2 * kk + hh) ^ (kr & 7))]);
+        const fa_bf16x8 kf = __builtin_bit_cast(fa_bf16x8, k_s[kr * 8 + ((2 * kk + hh) ^ ((kr >> 1) & 7))]);
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[b], 0, 0, 0);
       }
     }

@@ -14,8 +14,7 @@
 // Global loads run two steps ahead through two register stages: with one
 // workgroup per CU (the prefill shapes) a single step of look-ahead leaves the
 // MFMAs waiting on L2 latency. LDS rows are 128 B (64 bf16); the 16-byte chunk
-// c of row r lives at c ^ (r & 7), so the 32 rows read by one fragment load
-// spread over all banks.
+// c of row r lives at slot c ^ ((r / 2) % 8) (see swz).
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive
 // tiles along M (which share one B column block) go to the same XCD, so a
 // weight block is fetched from HBM into one L2 only.
@@ -47,7 +46,11 @@ struct GemmArgs {
   int splits;      // K ranges (1 = no split)
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ (row & 7)); }
+// A 16-byte LDS access of 16 lanes covers all 64 banks once when their 16
+// consecutive rows use 16 distinct (row parity, slot) pairs: the slot is
+// chunk ^ ((row / 2) % 8). (chunk ^ (row % 8) repeats every 8 rows, which put
+// rows r and r + 8 on the same banks: a 2-way conflict on every fragment read.)
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ ((row >> 1) & 7)); }
 
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
