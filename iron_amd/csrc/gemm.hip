@@ -8,18 +8,38 @@
 // host (B row-major (K, N) through a transpose, C column-major by swapping the
 // operands: C^T = B A^T).
 //
-// Tiling: 128x128 output tile per 256-thread workgroup, 4 waves in 2x2, each
-// wave owns 64x64 = 2x2 MFMA tiles (64 fp32 accumulators per lane). K advances
-// 64 per step through a double-buffered LDS ring (one barrier per step).
-// Global loads run two steps ahead through two register stages: with one
-// workgroup per CU (the prefill shapes) a single step of look-ahead leaves the
-// MFMAs waiting on L2 latency. LDS rows are 128 B (64 bf16); the 16-byte chunk
-// c of row r lives at slot c ^ ((r / 2) % 8) (see swz).
+// Tiles: a workgroup of WMW x WNW waves owns a (WMW*TI*32) x (WNW*TJ*32)
+// output tile; each wave owns TI x TJ MFMA tiles of 32x32. Four shapes are
+// instantiated and gemm_launch picks one with a cost model: 256x256 (8 waves
+// of 64x128), 256x128 (8 waves of 64x64), 128x128 with 8 waves of 64x32 (one
+// workgroup per CU, 3 steps of look-ahead) and 128x128 with 4 waves of 64x64
+// (two workgroups per CU). Bigger tiles fetch fewer bytes per flop: at ~64
+// B/clk of L2->CU fill per CU, a 128x128x64 step needs as many cycles to fill
+// as its MFMAs take, a 256x256 step half as many. Two waves per SIMD hide each
+// other's LDS and barrier waits, which matters most when each CU has a single
+// workgroup.
+//
+// K advances 64 per step through an NS-stage LDS ring filled by
+// global_load_lds_dwordx4: the loads write LDS directly, with no VGPR staging
+// and no ds_write (ds_write_b128 sustains ~73 B/clk per CU against ~205 B/clk
+// for ds_read_b128, and was the main loop's bottleneck). A stage holds the A
+// rows then the B rows, 128 B (64 bf16) each, in 1 KiB blocks of 8 rows; the
+// lane that lands on (row, slot) fetches chunk slot ^ ((row / 2) % 8), so
+// the 16-byte chunk c of row r sits at slot c ^ ((r / 2) % 8) (see swz).
+// Rows past M or N load row M-1 or N-1 instead: they only feed outputs that
+// are never stored.
+//
+// One barrier per step, placed after the step's last MFMAs are issued: those
+// MFMAs run while the wave waits for the next stage's loads and reads its
+// first fragments. Fragments are double-buffered in registers across the four
+// 16-deep k-slices of a step.
 // Tile order is XCD-aware: workgroup b runs on XCD b % 8, and consecutive
 // tiles along M (which share one B column block) go to the same XCD, so a
 // weight block is fetched from HBM into one L2 only.
 // Epilogue: round to bf16, then activation and clamp (the flm.GEMM order),
 // staged through LDS so global stores are 16-byte and row-contiguous.
+#include <algorithm>
+
 #include "iron_common.hpp"
 #include "../../include/iron_hip.h"
 
@@ -28,10 +48,11 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int kThreads = 256;
+constexpr int BK = 64;
 constexpr int kChunks = BK / 8;  // 16-byte chunks per LDS row
+constexpr int kSplitTile = 128;  // tile edge the split-K policy counts in
 
 struct GemmArgs {
   const uint16_t* A;  // (M, K)
@@ -46,137 +67,155 @@ struct GemmArgs {
   int splits;      // K ranges (1 = no split)
 };
 
+template <int WMW_, int WNW_, int TI_, int TJ_, int NS_>
+struct Tile {
+  static constexpr int WMW = WMW_, WNW = WNW_, TI = TI_, TJ = TJ_, NS = NS_;
+  static constexpr int kWaves = WMW * WNW, kThreads = 64 * kWaves;
+  static constexpr int BM = WMW * TI * 32, BN = WNW * TJ * 32;
+  static constexpr int kPerWave = (BM + BN) / 8 / kWaves;  // 1 KiB blocks each wave loads per step
+  static constexpr int kStage = (BM + BN) * kChunks;       // 16-byte slots per stage
+  static_assert((BM + BN) / 8 % kWaves == 0, "a stage's blocks must split evenly over the waves");
+  static_assert(BM * BN * 2 <= NS * kStage * 16, "the bf16 C tile must fit in the stages' LDS");
+};
+using TileL = Tile<4, 2, 2, 4, 2>;   // 256x256, 8 waves of 64x128, 128 KiB
+using TileM = Tile<4, 2, 2, 2, 2>;   // 256x128, 8 waves of 64x64, 96 KiB
+using TileS = Tile<2, 4, 2, 1, 4>;   // 128x128, 8 waves of 64x32, 128 KiB, 3 steps ahead
+using TileS2 = Tile<2, 2, 2, 2, 2>;  // 128x128, 4 waves of 64x64, 64 KiB: two workgroups per CU
+
 // A 16-byte LDS access of 16 lanes covers all 64 banks once when their 16
 // consecutive rows use 16 distinct (row parity, slot) pairs: the slot is
 // chunk ^ ((row / 2) % 8). (chunk ^ (row % 8) repeats every 8 rows, which put
 // rows r and r + 8 on the same banks: a 2-way conflict on every fragment read.)
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + (chunk ^ ((row >> 1) & 7)); }
 
-typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+// Wait until at most N of this wave's global loads are outstanding, then
+// barrier. (__syncthreads would wait for all of them.) The memory clobber
+// keeps LDS reads of the next stage below the barrier.
+template <int N>
+__device__ __forceinline__ void wait_loads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
-// One step's global loads into register stage r (4 A + 4 B chunks per
-// thread). GUARD zero-fills rows past M / N; steps past the end reload the
-// last step (never stored).
-#define IRON_GEMM_LOAD_CHUNK(r, i, k0)                                                                   \
-  {                                                                                                      \
-    const int id_ = tid + (i) * kThreads, row_ = id_ >> 3, c_ = id_ & 7;                                 \
-    const int gm_ = m0 + row_, gn_ = n0 + row_;                                                          \
-    r[i] = (!GUARD || gm_ < a.M) ? *reinterpret_cast<const u32x4v*>(Ag + static_cast<size_t>(gm_) * a.K +   \
-                                                                     (k0) + c_ * 8)                       \
-                                 : u32x4v{0, 0, 0, 0};                                                   \
-    r[4 + (i)] = (!GUARD || gn_ < a.N) ? *reinterpret_cast<const u32x4v*>(Bg + static_cast<size_t>(gn_) *  \
-                                                                          a.K + (k0) + c_ * 8)           \
-                                       : u32x4v{0, 0, 0, 0};                                             \
-  }
-#define IRON_GEMM_LOAD(r, step)                                                                          \
-  {                                                                                                      \
-    const int k0_ = min(step, nk - 1) * BK;                                                              \
-    IRON_GEMM_LOAD_CHUNK(r, 0, k0_) IRON_GEMM_LOAD_CHUNK(r, 1, k0_)                                      \
-    IRON_GEMM_LOAD_CHUNK(r, 2, k0_) IRON_GEMM_LOAD_CHUNK(r, 3, k0_)                                      \
-  }
-#define IRON_GEMM_STORE_CHUNK(r, i, As_, Bs_)                                                            \
-  {                                                                                                      \
-    const int id_ = tid + (i) * kThreads, row_ = id_ >> 3, c_ = id_ & 7;                                 \
-    As_[swz(row_, c_)] = r[i];                                                                           \
-    Bs_[swz(row_, c_)] = r[4 + (i)];                                                                     \
-  }
-#define IRON_GEMM_STORE(r, buf)                                                                          \
-  {                                                                                                      \
-    u32x4v* As_ = reinterpret_cast<u32x4v*>(smem + (buf) * 2 * BM * kChunks);                            \
-    u32x4v* Bs_ = As_ + BM * kChunks;                                                                    \
-    IRON_GEMM_STORE_CHUNK(r, 0, As_, Bs_) IRON_GEMM_STORE_CHUNK(r, 1, As_, Bs_)                          \
-    IRON_GEMM_STORE_CHUNK(r, 2, As_, Bs_) IRON_GEMM_STORE_CHUNK(r, 3, As_, Bs_)                          \
-  }
-// 4 k-slices of 16: per slice each wave reads 2 A and 2 B fragments (one
-// 16-byte LDS read each) and issues its 2x2 MFMAs.
-#define IRON_GEMM_COMPUTE(buf)                                                                           \
-  {                                                                                                      \
-    const uint4* As_ = smem + (buf) * 2 * BM * kChunks;                                                  \
-    const uint4* Bs_ = As_ + BM * kChunks;                                                               \
-    _Pragma("unroll") for (int kk = 0; kk < BK / 16; ++kk) {                                             \
-      const int c_ = kk * 2 + (lane >> 5);                                                               \
-      bf16x8_t fa[2], fb[2];                                                                             \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i) {                                                    \
-        fa[i] = __builtin_bit_cast(bf16x8_t, As_[swz(wm * 64 + i * 32 + (lane & 31), c_)]);              \
-        fb[i] = __builtin_bit_cast(bf16x8_t, Bs_[swz(wn * 64 + i * 32 + (lane & 31), c_)]);              \
-      }                                                                                                  \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                                      \
-      _Pragma("unroll") for (int j = 0; j < 2; ++j)                                                      \
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);           \
-    }                                                                                                    \
-  }
-
-template <bool GUARD>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
-  __shared__ uint4 smem[2 * 2 * BM * kChunks];  // [buf][A|B][row][chunk] = 64 KiB
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+template <class T>
+__global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
+  constexpr int BM = T::BM, BN = T::BN, TI = T::TI, TJ = T::TJ, NS = T::NS, PW = T::kPerWave;
+  __shared__ u32x4v smem[NS * T::kStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / T::WNW, wn = wave % T::WNW;
 
   // XCD-aware tile order (over tiles x K ranges)
   const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
-  const int T = tiles_m * tiles_n * a.splits;
+  const int nt = tiles_m * tiles_n * a.splits;
   int t = blockIdx.x;
-  if (T % 8 == 0) t = (t % 8) * (T / 8) + t / 8;
+  if (nt % 8 == 0) t = (t % 8) * (nt / 8) + t / 8;
   const int kb = t / (tiles_m * tiles_n);
   t %= tiles_m * tiles_n;
   const int tm = t % tiles_m, tn = t / tiles_m;
   const int m0 = tm * BM, n0 = tn * BN;
   const int nk = a.K / BK / a.splits;  // steps in this workgroup's K range
-  const uint16_t* Ag = a.A + static_cast<size_t>(kb) * nk * BK;
-  const uint16_t* Bg = a.B + static_cast<size_t>(kb) * nk * BK;
 
-  f32x16_t acc[2][2];
+  // The PW blocks this wave loads each step: block b < BM/8 is rows 8b..8b+7
+  // of A, the rest are rows of B. Source pointers at the first step of the range.
+  const uint16_t* src[PW];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int j = 0; j < PW; ++j) {
+    const int b = wave * PW + j;
+    const bool is_a = b < BM / 8;
+    const int row = (is_a ? b : b - BM / 8) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    const size_t k0 = static_cast<size_t>(kb) * nk * BK + chunk * 8;
+    src[j] = is_a ? a.A + static_cast<size_t>(min(m0 + row, a.M - 1)) * a.K + k0
+                  : a.B + static_cast<size_t>(min(n0 + row, a.N - 1)) * a.K + k0;
+  }
+  auto issue = [&](int step) {
+    u32x4v* st = smem + (step % NS) * T::kStage;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < PW; ++j)
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + step * BK),
+                                       reinterpret_cast<unsigned*>(st + (wave * PW + j) * 64), 16, 0, 0);
+  };
+
+  f32x16_t acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  // two register stages: steps s+1 and s+2 are in flight while step s computes
-  u32x4v st0[8], st1[8];
-  IRON_GEMM_LOAD(st0, 0);
-  IRON_GEMM_LOAD(st1, 1);
-  IRON_GEMM_STORE(st0, 0);
-  __syncthreads();
-  for (int it = 0; it < nk; it += 2) {
-    IRON_GEMM_LOAD(st0, it + 2);
-    IRON_GEMM_COMPUTE(0);  // step it
-    if (it + 1 < nk) IRON_GEMM_STORE(st1, 1);
-    __syncthreads();
-    if (it + 1 < nk) {
-      IRON_GEMM_LOAD(st1, it + 3);
-      IRON_GEMM_COMPUTE(1);  // step it + 1
-      if (it + 2 < nk) IRON_GEMM_STORE(st0, 0);
-      __syncthreads();
+  bf16x8_t fa[2][TI], fb[2][TJ];
+  auto read_frags = [&](int set, int stage, int kk) {
+    const u32x4v* As = smem + stage * T::kStage;
+    const u32x4v* Bs = As + BM * kChunks;
+    const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+      fa[set][i] = __builtin_bit_cast(bf16x8_t, As[swz(wm * TI * 32 + i * 32 + (lane & 31), c)]);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+      fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[swz(wn * TJ * 32 + j * 32 + (lane & 31), c)]);
+  };
+
+  // prologue: steps 0..NS-2 in flight, wait for step 0, first fragments
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < nk) issue(p);
+  if (NS - 1 < nk)
+    wait_loads_barrier<PW * (NS - 2)>();
+  else
+    wait_loads_barrier<0>();
+  read_frags(0, 0, 0);
+
+  for (int s = 0; s < nk; ++s) {
+    // the stage read in step s-1: every wave passed the barrier after its last read of it
+    if (s + NS - 1 < nk) issue(s + NS - 1);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int cur = kk & 1, nxt = cur ^ 1;
+      if (kk + 1 < BK / 16) read_frags(nxt, s % NS, kk + 1);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+      if (kk + 1 == BK / 16 && s + 1 < nk) {
+        // steps s+2..min(s+NS-1, nk-1) may stay in flight
+        if (s + NS - 1 < nk)
+          wait_loads_barrier<PW * (NS - 2)>();
+        else
+          wait_loads_barrier<0>();
+        read_frags(nxt, (s + 1) % NS, 0);
+      }
     }
   }
 
   if (a.partial) {  // split-K: raw fp32 sums straight from the accumulators
     float* P = a.partial + static_cast<size_t>(kb) * a.M * a.N;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int gm = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          const int gn = n0 + wn * 64 + j * 32 + (lane & 31);
-          if (!GUARD || (gm < a.M && gn < a.N)) P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
+          const int gm = m0 + wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const int gn = n0 + wn * TJ * 32 + j * 32 + (lane & 31);
+          if (gm < a.M && gn < a.N) P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
         }
     return;
   }
 
-  // epilogue through LDS: C tile as bf16 [128][128] (32 KiB)
+  // epilogue through LDS: C tile as bf16 [BM][BN]
+  __syncthreads();  // every wave is done reading the last stage
   uint16_t* Cs = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int col = wn * 64 + j * 32 + (lane & 31);
+        const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int col = wn * TJ * 32 + j * 32 + (lane & 31);
         float x = acc[i][j][v];
         if (a.epi != EPI_NONE || a.clamp) {
           x = bf16_to_f32(f32_to_bf16(x));
@@ -188,10 +227,10 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
   __syncthreads();
   const bool full_n = (n0 + BN <= a.N) && (a.ldc % 8 == 0);
 #pragma unroll
-  for (int i = 0; i < (BM * BN / 8) / kThreads; ++i) {
-    const int id = tid + i * kThreads, row = id >> 4, c = id & 15;
+  for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
+    const int id = tid + i * T::kThreads, row = id / (BN / 8), c = id % (BN / 8);
     const int gm = m0 + row, gn = n0 + c * 8;
-    if (gm >= a.M) continue;
+    if (gm >= a.M || gn >= a.N) continue;
     const uint4 v = reinterpret_cast<const uint4*>(Cs)[row * (BN / 8) + c];
     uint16_t* dst = a.C + static_cast<size_t>(gm) * a.ldc + gn;
     if (full_n) {
@@ -203,12 +242,6 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(GemmArgs a) {
     }
   }
 }
-
-#undef IRON_GEMM_LOAD_CHUNK
-#undef IRON_GEMM_LOAD
-#undef IRON_GEMM_STORE_CHUNK
-#undef IRON_GEMM_STORE
-#undef IRON_GEMM_COMPUTE
 
 // Split-K merge: C = clamp(act(bf16(sum_kb partial[kb]))), the same epilogue
 // order as the single-pass kernel. One thread per output element.
@@ -261,19 +294,47 @@ static int gemm_check(const char* fn, const void* A, const void* B, const void* 
   return 0;
 }
 
+template <class T>
+static long long tile_count(const GemmArgs& a) {
+  return static_cast<long long>((a.M + T::BM - 1) / T::BM) * ((a.N + T::BN - 1) / T::BN) * a.splits;
+}
+
+// Cost model: a launch takes ceil(tiles / slots) rounds, each costing a full
+// round of tile work at the shape's measured full-occupancy rate (TF/s on one
+// MI355X: 256x256 ~1000, 256x128 ~900, 128x128/4 waves ~800, 128x128/8 waves
+// ~660). Slots are workgroups resident at once: one per CU, two for the 64 KiB
+// shape. Fewer, bigger tiles win on large problems; a problem of one round of
+// 128x128 tiles gets the 8-wave shape.
+template <class T>
+static double launch_cost(const GemmArgs& a, int per_cu, double tflops) {
+  const long long slots = 256LL * per_cu, rounds = (tile_count<T>(a) + slots - 1) / slots;
+  return static_cast<double>(rounds * slots) * T::BM * T::BN / tflops;
+}
+
+template <class T>
+static void launch_tile(const GemmArgs& a, hipStream_t s) {
+  IRON_LAUNCH(gemm_nt_kernel<T>, dim3(static_cast<unsigned>(tile_count<T>(a))), dim3(T::kThreads), 0, s, a);
+}
+
 static void gemm_launch(const GemmArgs& a, hipStream_t s) {
-  const long long tiles = static_cast<long long>((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN) * a.splits;
-  if (a.M % BM == 0 && a.N % BN == 0)
-    IRON_LAUNCH(gemm_nt_kernel<false>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, s, a);
+  const double cl = launch_cost<TileL>(a, 1, 1000.0), cm = launch_cost<TileM>(a, 1, 900.0);
+  const double cs = launch_cost<TileS>(a, 1, 660.0), cs2 = launch_cost<TileS2>(a, 2, 800.0);
+  const double best = std::min(std::min(cl, cm), std::min(cs, cs2));
+  if (cs == best)
+    launch_tile<TileS>(a, s);
+  else if (cl == best)
+    launch_tile<TileL>(a, s);
+  else if (cm == best)
+    launch_tile<TileM>(a, s);
   else
-    IRON_LAUNCH(gemm_nt_kernel<true>, dim3(static_cast<unsigned>(tiles)), dim3(kThreads), 0, s, a);
+    launch_tile<TileS2>(a, s);
 }
 
 extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K, long long ldc,
                                  int epilogue, int has_clamp, float clamp_lo, float clamp_hi, void* stream) {
   if (int rc = gemm_check("iron_gemm_bf16_nt", A, B, C, M, N, K, ldc, epilogue, has_clamp, clamp_lo, clamp_hi))
     return rc;
-  const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile);
   IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt: problem too large");
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, nullptr, 1};
@@ -285,7 +346,7 @@ extern "C" int iron_gemm_splitk_choose(int M, int N, int K) {
   // Split K while the workgroups stay within 1.25x the 256 CUs and every K range
   // keeps >= 8 steps of 64; at most 8 ranges.
   if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 1;
-  const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile);
   int s = 1;
   while (s < 8 && tiles * s * 2 <= 320 && (K / BK) % (s * 2) == 0 && K / BK / (s * 2) >= 8) s *= 2;
   return s;
@@ -310,7 +371,7 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
   IRON_REQUIRE(workspace && workspace_bytes >= need, "iron_gemm_bf16_nt_splitk: workspace of %lld bytes < %lld",
                workspace_bytes, need);
   IRON_REQUIRE(aligned16(workspace), "iron_gemm_bf16_nt_splitk: workspace must be 16-byte aligned");
-  const long long tiles = static_cast<long long>((M + BM - 1) / BM) * ((N + BN - 1) / BN) * splits;
+  const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile) * splits;
   IRON_REQUIRE(tiles < (1LL << 31) && static_cast<long long>(M) * N < (1LL << 38),
                "iron_gemm_bf16_nt_splitk: problem too large");
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,

@@ -99,6 +99,37 @@ def test_prefill_gemm_shapes(gpu, M, K, N):
     assert not bad, bad[:5]
 
 
+@pytest.mark.parametrize(
+    "M,K,N",
+    [
+        (4000, 128, 4104),  # 256x256 tiles, ragged M and N
+        (4096, 256, 4100),  # 256x256 tiles, odd row stride: element stores
+        (3968, 2048, 2048),  # 256x128 tiles (prefill o_proj at 3968 tokens)
+        (2600, 64, 3300),  # 256x128 tiles, ragged, odd row stride
+        (1280, 192, 4096),  # 128x128 tiles, more workgroups than CUs
+        (1000, 192, 2050),  # 128x128 tiles, one workgroup per CU, ragged
+    ],
+)
+def test_gemm_tile_shapes(gpu, M, K, N):
+    """Each tile shape the launcher picks (by tile count), at ragged edges
+    (rows past M or N load the last row; their outputs are never stored):
+    within one bf16 ulp of the fp32-accumulated product."""
+    from iron_amd import _lib
+
+    gen = torch.Generator().manual_seed(M * 7 + K + N)
+    A = torch.randn(M, K, generator=gen).to(BF16)
+    W = (torch.randn(N, K, generator=gen) * 0.05).to(BF16)
+    ref = A.float() @ W.float().T
+    C = torch.full((M, N), float("nan"), dtype=BF16, device=gpu)
+    Ad, Wd = A.to(gpu), W.to(gpu)  # held until the launch has run
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+              _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    assert not torch.isnan(C).any()
+    bad = ops.within_bf16_ulps(C, ref, n_ulp=1.0, atol=1e-5 * float(ref.abs().max()))
+    assert not bad, bad[:5]
+
+
 @pytest.mark.parametrize("M,K,N,splits", [(512, 8192, 2048, 4), (512, 2048, 2048, 4), (512, 2048, 3072, 2),
                                           (100, 512, 200, 2), (256, 1024, 384, 8), (64, 4096, 64, 8)])
 @pytest.mark.parametrize("epi,clamp", [(0, False), (2, False), (4, True)])
