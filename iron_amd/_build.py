@@ -44,6 +44,12 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file additions. attention.hip: keep MFMA accumulators in VGPRs. The
+# flash-attention loop rescales its output accumulators with VALU ops, and with
+# accumulators in AGPRs the compiler copied them back and forth every block.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -53,7 +59,7 @@ def _hipcc() -> str:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

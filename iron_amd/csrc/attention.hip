@@ -303,15 +303,22 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 // MFMA (v_mfma_f32_32x32x16_bf16).
 //
 // Workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries and
-// walks the visible keys in blocks of 64 staged in LDS (K row-major with the
-// 16-byte chunk at slot chunk ^ ((key / 2) % 8), which keeps the 16 lanes of
-// a fragment read on distinct banks; V transposed to [dim][key]). Per block a wave
-// computes S^T = K Q^T (two 32x32 tiles): every lane then holds one query
-// column (lane % 32) and 16 keys, so the softmax row statistics need only the
-// lane's own registers and one exchange with lane ^ 32. The probabilities go
-// to bf16 and feed O^T += V^T P^T directly from registers as the B operand;
-// the k index of that product is a permutation of the block's keys that
-// matches the S^T accumulator layout, and V^T is read in the same order.
+// walks the visible keys in blocks of 64. K and V blocks are staged row-major
+// in a 3-stage LDS ring filled by global_load_lds_dwordx4 (no VGPR staging, no
+// LDS stores), two blocks ahead of the one being computed, one barrier per
+// block. Per block a wave computes S^T = K Q^T (two 32x32 tiles): every lane
+// then holds one query column (lane % 32) and 16 keys, so the softmax row
+// statistics need only the lane's own registers and one exchange with lane ^ 32.
+// The probabilities go to bf16 and feed O^T += V^T P^T directly from registers
+// as the B operand; the k index of that product is a permutation of the
+// block's keys that matches the S^T accumulator layout. The V^T operand comes
+// straight from the row-major V block through ds_read_b64_tr_b16: in each
+// 16-lane group, lane i receives element i % 4 of the 8-byte rows addressed by
+// lanes 4j + i / 4 (j = 0..3), so lanes addressing 4 keys x 16 dims receive 16
+// dims x 4 keys. K rows keep the 16-byte chunk c at slot c ^ ((key / 2) % 8)
+// (16 rows of a ds_read_b128 on distinct banks); V rows at slot
+// c ^ (((key / 2) % 4) * 2), which separates rows r and r + 2 of a transposed
+// read (their chunk pair {c, c + 1} moves to another pair of slots).
 // Online softmax in the log2 domain, fp32 statistics; output rows in
 // [Sq, out_rows) are zero-filled (the MHA operator's padding).
 // ---------------------------------------------------------------------------
@@ -336,19 +343,54 @@ typedef float fa_f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int fa_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int fa_u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kFaQ = 128;      // queries per workgroup (4 waves x 32)
-constexpr int kFaK = 64;       // keys per block
-constexpr int kVtStride = 68;  // V^T row: 64 keys + 4 pad (136 B: 8-byte reads of 32 rows hit distinct banks)
-constexpr int kOutStride = 72; // output staging row (144 B)
-constexpr int kFaLds = (kFaK * 128 + kD * kVtStride * 2) > (4 * 32 * kOutStride * 2)
-                           ? (kFaK * 128 + kD * kVtStride * 2)
-                           : (4 * 32 * kOutStride * 2);
+typedef short fa_i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFaQ = 128;             // queries per workgroup (4 waves x 32)
+constexpr int kFaK = 64;              // keys per block
+constexpr int kFaStages = 4;          // K/V blocks resident (see the pipeline in the kernel)
+constexpr int kFaBlock = kFaK * 128;  // bytes of a 64-row K (or V) block
+constexpr int kOutStride = 72;        // output staging row (144 B)
+constexpr int kFaLds = (kFaStages * 2 * kFaBlock) > (4 * 32 * kOutStride * 2) ? (kFaStages * 2 * kFaBlock)
+                                                                               : (4 * 32 * kOutStride * 2);
+
+// Lanes l and l ^ 32 exchange values in one VALU op (v_permlane32_swap_b32
+// swaps the upper half of its first operand with the lower half of its
+// second): with both operands x, the two results hold x[l] and x[l ^ 32] in
+// every lane. Inline assembly, because the compiler's builtin for it kept only
+// the first of the two results here. The s_nop covers the VALU-write to
+// permlane-read hazard (the compiler emits the same before the builtin).
+__device__ __forceinline__ void fa_pair(float x, float& r0, float& r1) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float fa_pair_max(float x) {
+  float r0, r1;
+  fa_pair(x, r0, r1);
+  return fmaxf(r0, r1);
+}
+__device__ __forceinline__ float fa_pair_sum(float x) {
+  float r0, r1;
+  fa_pair(x, r0, r1);
+  return r0 + r1;
+}
+
+__device__ __forceinline__ int fa_k_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int fa_v_slot(int row, int chunk) { return chunk ^ (((row >> 1) & 3) << 1); }
+
+// Wait until at most N of this wave's global loads are outstanding, then
+// barrier (__syncthreads would wait for all of them). The memory clobber keeps
+// the next stage's LDS reads below the barrier.
+template <int N>
+__device__ __forceinline__ void fa_wait_loads_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
 
 __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kFaLds];
-  fa_u32x4* k_s = reinterpret_cast<fa_u32x4*>(lds);                 // [key][chunk ^ ((key / 2) % 8)]
-  uint16_t* vt_s = reinterpret_cast<uint16_t*>(lds + kFaK * 128);   // [dim][key]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
   const int h = blockIdx.y, hk = h / (a.H / a.Hkv);
   const int q0 = blockIdx.x * kFaQ;
@@ -379,95 +421,195 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   const int qpos = a.q_offset + qw + c;  // absolute position of this lane's query
   int kend = a.Skv;
   if (a.causal) kend = min(kend, a.q_offset + min(q0 + kFaQ, a.Sq));
+  const int nb = (kend + kFaK - 1) / kFaK;
   const int wave_last = a.q_offset + min(qw + 31, a.Sq - 1);
+  const int wave_first = a.q_offset + qw;  // keys <= it are visible to every query of the wave
 
-  for (int k0 = 0; k0 < kend; k0 += kFaK) {
-    __syncthreads();  // the previous block's LDS reads are done
-    for (int e = tid; e < kFaK * 8; e += 256) {
-      const int kr = e >> 3, ch = e & 7, key = k0 + kr;
-      fa_u32x4 kt = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      if (key < a.Skv) {
-        kt = *reinterpret_cast<const fa_u32x4*>(a.k + hk * a.k_hs + static_cast<long long>(key) * a.k_rs + ch * 8);
-        vv = *reinterpret_cast<const fa_u32x4*>(a.v + hk * a.v_hs + static_cast<long long>(key) * a.v_rs + ch * 8);
-      }
-      k_s[kr * 8 + (ch ^ ((kr >> 1) & 7))] = kt;
+  // Loader: a stage is [K block][V block], each 8 x 1 KiB of 8 rows; wave w
+  // loads 1 KiB blocks 4w..4w+3 (0-7 K, 8-15 V). Lane l lands on row
+  // 8 (b % 8) + l / 8, slot l % 8 and fetches the chunk that belongs there.
+  // Keys past Skv load key Skv-1: finite values whose weights are zero.
+  const uint16_t* src[4];
+  long long rstride[4];
+  int lrow[4];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        vt_s[(ch * 8 + 2 * w) * kVtStride + kr] = static_cast<uint16_t>(vv[w] & 0xffffu);
-        vt_s[(ch * 8 + 2 * w + 1) * kVtStride + kr] = static_cast<uint16_t>(vv[w] >> 16);
-      }
+  for (int j = 0; j < 4; ++j) {
+    const int b = wave * 4 + j;
+    const bool is_k = b < 8;
+    const int r = (b & 7) * 8 + (lane >> 3), slot = lane & 7;
+    const int chunk = is_k ? fa_k_slot(r, slot) : fa_v_slot(r, slot);  // both are involutions
+    src[j] = (is_k ? a.k + hk * a.k_hs : a.v + hk * a.v_hs) + chunk * 8;
+    rstride[j] = is_k ? a.k_rs : a.v_rs;
+    lrow[j] = r;
+  }
+  auto issue = [&](int bi) {
+    unsigned char* st = lds + (bi % kFaStages) * 2 * kFaBlock;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = min(bi * kFaK + lrow[j], a.Skv - 1);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + key * rstride[j]),
+                                       reinterpret_cast<unsigned*>(st + (wave * 4 + j) * 1024), 16, 0, 0);
     }
-    __syncthreads();
-    if (a.causal && k0 > wave_last) continue;  // every key of the block is after this wave's queries
+  };
+  // this lane's transposed-read address inside a V block: 16-lane group g
+  // covers dims 16 (g % 2) .. + 15 (+ 32 db) and keys 4 hh .. + 3 (+ 16 st, + 8)
+  const int tr_row = 4 * hh + ((lane & 15) >> 2), tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-    // S^T = K Q^T: s[b][j] is key k0 + 32 b + 8 (j / 4) + 4 hh + j % 4, query qw + c
-    fa_f32x16 s[2];
+  // S^T = K Q^T for block bi: sc[b][j] is key 64 bi + 32 b + 8 (j / 4) + 4 hh + j % 4, query qw + c
+  auto scores = [&](int bi, fa_f32x16 (&sc)[2]) {
+    const unsigned char* ks = lds + (bi % kFaStages) * 2 * kFaBlock;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) s[b][j] = 0.f;
+      for (int j = 0; j < 16; ++j) sc[b][j] = 0.f;
       const int kr = 32 * b + c;
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const fa_bf16x8 kf = __builtin_bit_cast(fa_bf16x8, k_s[kr * 8 + ((2 * kk + hh) ^ ((kr >> 1) & 7))]);
-        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[b], 0, 0, 0);
+        const fa_bf16x8 kf = __builtin_bit_cast(
+            fa_bf16x8, *reinterpret_cast<const fa_u32x4*>(ks + kr * 128 + fa_k_slot(kr, 2 * kk + hh) * 16));
+        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[b], 0, 0, 0);
       }
     }
-    float mx = -INFINITY;
+  };
+  auto visible = [&](int bi) { return !a.causal || bi * kFaK <= wave_last; };
+
+  // Software pipeline over key blocks: iteration bi waits for block bi+1,
+  // issues its S^T MFMAs, then runs block bi's softmax and P V while they
+  // execute. Stages: bi (V being read), bi+1 (K being read), bi+2 in flight,
+  // bi+3 being issued into the stage block bi-1 used.
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+  for (int p = 0; p < kFaStages - 1; ++p)
+    if (p < nb) issue(p);
+  static_assert(kFaStages == 4, "the wait counts below assume 4 stages");
+  if (nb >= 3)
+    fa_wait_loads_barrier<8>();
+  else if (nb == 2)
+    fa_wait_loads_barrier<4>();
+  else
+    fa_wait_loads_barrier<0>();
+  fa_f32x16 sa[2], sb[2];
+  if (visible(0)) scores(0, sa);
+
+  auto step = [&](int bi, fa_f32x16 (&cur)[2], fa_f32x16 (&nxt)[2]) {
+    if (bi + 1 < nb) {
+      if (bi + 2 < nb)
+        fa_wait_loads_barrier<4>();
+      else
+        fa_wait_loads_barrier<0>();
+      // block bi-1's stage is free: every wave passed this barrier after its last read of it
+      if (bi + kFaStages - 1 < nb) issue(bi + kFaStages - 1);
+      if (visible(bi + 1)) scores(bi + 1, nxt);
+    }
+    if (!visible(bi)) return;  // every key of the block is after this wave's queries
+    const int k0 = bi * kFaK;
+    const unsigned char* vs = lds + (bi % kFaStages) * 2 * kFaBlock + kFaBlock;
+      // V^T fragments for O^T += V^T P^T, read while the next block's S^T MFMAs run: k-step st,
+      // element i of lane (d, hh) is key 16 st + 8 (i / 4) + 4 hh + i % 4 (two
+      // transposed reads of 4 keys each). The reads are inline assembly ending in
+      // their own lgkmcnt wait: as a builtin, the compiler makes the first one wait
+      // for every LDS-direct load in flight (it cannot tell the stages apart).
+      fa_u32x2 vt[2][4][2];
+      {
+        const unsigned vb = static_cast<unsigned>(reinterpret_cast<uintptr_t>(vs));
+        unsigned ad[2][4][2];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = k0 + 32 * b + 8 * (j >> 2) + 4 * hh + (j & 3);
-        const bool vis = key < a.Skv && (!a.causal || key <= qpos);
-        const float v = vis ? s[b][j] * a.scale_log2 : -INFINITY;
-        s[b][j] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m - mnew);
-    // P^T fragments: pf[2 b + sp] element i = register 8 sp + i of s[b]
-    fa_bf16x8 pf[4];
-    float psum = 0.f;
+        for (int db = 0; db < 2; ++db) {
+          const int dim = 32 * db + tr_dim;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+          for (int st = 0; st < 4; ++st)
 #pragma unroll
-      for (int sp = 0; sp < 2; ++sp) {
-        float p[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float x = s[b][8 * sp + i];
-          p[i] = (x == -INFINITY) ? 0.f : exp2f(x - mnew);
-          psum += p[i];
+            for (int hl = 0; hl < 2; ++hl) {
+              const int r = 16 * st + 8 * hl + tr_row;
+              ad[db][st][hl] = vb + r * 128 + fa_v_slot(r, dim >> 3) * 16 + (dim & 7) * 2;
+            }
         }
-        const fa_u32x4 w = {cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
-                            cvt_pk_bf16(p[6], p[7])};
-        pf[2 * b + sp] = __builtin_bit_cast(fa_bf16x8, w);
+        asm volatile(
+            "ds_read_b64_tr_b16 %0, %16\n\tds_read_b64_tr_b16 %1, %17\n\t"
+            "ds_read_b64_tr_b16 %2, %18\n\tds_read_b64_tr_b16 %3, %19\n\t"
+            "ds_read_b64_tr_b16 %4, %20\n\tds_read_b64_tr_b16 %5, %21\n\t"
+            "ds_read_b64_tr_b16 %6, %22\n\tds_read_b64_tr_b16 %7, %23\n\t"
+            "ds_read_b64_tr_b16 %8, %24\n\tds_read_b64_tr_b16 %9, %25\n\t"
+            "ds_read_b64_tr_b16 %10, %26\n\tds_read_b64_tr_b16 %11, %27\n\t"
+            "ds_read_b64_tr_b16 %12, %28\n\tds_read_b64_tr_b16 %13, %29\n\t"
+            "ds_read_b64_tr_b16 %14, %30\n\tds_read_b64_tr_b16 %15, %31\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(vt[0][0][0]), "=&v"(vt[0][0][1]), "=&v"(vt[0][1][0]), "=&v"(vt[0][1][1]), "=&v"(vt[0][2][0]),
+              "=&v"(vt[0][2][1]), "=&v"(vt[0][3][0]), "=&v"(vt[0][3][1]), "=&v"(vt[1][0][0]), "=&v"(vt[1][0][1]),
+              "=&v"(vt[1][1][0]), "=&v"(vt[1][1][1]), "=&v"(vt[1][2][0]), "=&v"(vt[1][2][1]), "=&v"(vt[1][3][0]),
+              "=&v"(vt[1][3][1])
+            : "v"(ad[0][0][0]), "v"(ad[0][0][1]), "v"(ad[0][1][0]), "v"(ad[0][1][1]), "v"(ad[0][2][0]),
+              "v"(ad[0][2][1]), "v"(ad[0][3][0]), "v"(ad[0][3][1]), "v"(ad[1][0][0]), "v"(ad[1][0][1]),
+              "v"(ad[1][1][0]), "v"(ad[1][1][1]), "v"(ad[1][2][0]), "v"(ad[1][2][1]), "v"(ad[1][3][0]),
+              "v"(ad[1][3][1]));
       }
-    l = l * alpha + psum;
-    m = mnew;
+      // Online softmax in the log2 domain with c = scale * log2(e) > 0: the row
+      // maximum is taken on the raw scores, p = 2^(s c - m) is one FMA and one
+      // v_exp_f32. Only blocks that cross Skv or the causal diagonal of this
+      // wave's queries are masked, and O is rescaled only when some lane's
+      // maximum moved: the softmax VALU work, not the MFMAs, bounds this loop.
+      const float cs = a.scale_log2;
+      float mx = -INFINITY;
+      if (k0 + kFaK > a.Skv || (a.causal && k0 + kFaK - 1 > wave_first)) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      o[0][j] *= alpha;
-      o[1][j] *= alpha;
-    }
-    // O^T += V^T P^T over the block's 64 keys, 4 k-steps of 16 in the permuted key order
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      const uint16_t* vrow = vt_s + (32 * db + c) * kVtStride;
+          for (int j = 0; j < 16; ++j) {
+            const int key = k0 + 32 * b + 8 * (j >> 2) + 4 * hh + (j & 3);
+            const bool vis = key < a.Skv && (!a.causal || key <= qpos);
+            cur[b][j] = vis ? cur[b][j] : -INFINITY;
+            mx = fmaxf(mx, cur[b][j]);
+          }
+      } else {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int kb = 16 * st + 4 * hh;  // keys kb..kb+3 and kb+8..kb+11 (32 (st / 2) + 16 (st % 2) = 16 st)
-        const fa_u32x2 lo = *reinterpret_cast<const fa_u32x2*>(vrow + kb);
-        const fa_u32x2 hi = *reinterpret_cast<const fa_u32x2*>(vrow + kb + 8);
-        const fa_u32x4 vw = {lo.x, lo.y, hi.x, hi.y};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(fa_bf16x8, vw), pf[st], o[db], 0, 0, 0);
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int j = 0; j < 16; j += 2) mx = fmaxf(mx, fmaxf(cur[b][j], cur[b][j + 1]));  // v_max3_f32
       }
-    }
+      mx = fa_pair_max(mx);
+      const float mnew = fmaxf(m, mx * cs);
+      const float moff = (mnew == -INFINITY) ? 0.f : mnew;  // keeps 2^(-inf - moff) = 0, never NaN
+      const float alpha = __builtin_amdgcn_exp2f(m - moff);  // 0 on the first visible block
+      // P^T fragments: pf[2 b + sp] element i = register 8 sp + i of s[b]
+      fa_bf16x8 pf[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) {
+          float p[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(cur[b][8 * sp + i], cs, -moff));
+          const fa_u32x4 w = {cvt_pk_bf16(p[0], p[1]), cvt_pk_bf16(p[2], p[3]), cvt_pk_bf16(p[4], p[5]),
+                              cvt_pk_bf16(p[6], p[7])};
+          // the row sum of the bf16 weights the PV product uses, two per v_dot2
+#pragma unroll
+          for (int i = 0; i < 4; ++i) psum = dot2_bf16(w[i], 0x3f803f80u, psum);
+          pf[2 * b + sp] = __builtin_bit_cast(fa_bf16x8, w);
+        }
+      l = l * alpha + psum;
+      m = mnew;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          o[0][j] *= alpha;
+          o[1][j] *= alpha;
+        }
+      }
+      // O^T += V^T P^T over the block's 64 keys, 4 k-steps of 16
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const fa_u32x4 vw = {vt[db][st][0].x, vt[db][st][0].y, vt[db][st][1].x, vt[db][st][1].y};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(fa_bf16x8, vw), pf[st], o[db], 0, 0, 0);
+        }
+  };
+  for (int bi = 0; bi < nb; bi += 2) {
+    step(bi, sa, sb);
+    if (bi + 1 < nb) step(bi + 1, sb, sa);
   }
 
-  l += __shfl_xor(l, 32, kWave);  // the two halves summed different keys of the same query
+  l = fa_pair_sum(l);  // the two halves summed different keys of the same query
   const float inv = l > 0.f ? 1.f / l : 0.f;
   __syncthreads();  // every wave is done with the K/V tiles
   uint16_t* stg = reinterpret_cast<uint16_t*>(lds) + wave * 32 * kOutStride;
@@ -574,6 +716,8 @@ extern "C" int iron_attention_prefill(const void* q, const void* k, const void* 
                "iron_attention_prefill: n_heads=%d must be a multiple of n_kv_heads=%d", n_heads, n_kv_heads);
   IRON_REQUIRE(seq_q > 0 && seq_kv > 0, "iron_attention_prefill: empty sequence");
   IRON_REQUIRE(q_offset >= 0, "iron_attention_prefill: q_offset must be >= 0");
+  IRON_REQUIRE(scale > 0.f && scale < INFINITY, "iron_attention_prefill: scale=%g must be positive and finite",
+               static_cast<double>(scale));
   if (out_rows < seq_q) out_rows = seq_q;
   IRON_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && q_row_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                    kv_row_stride % 8 == 0 && kv_head_stride % 8 == 0,

@@ -102,3 +102,41 @@ def test_mha_causal(gpu, seq_len, heads, kv):
     errs = ops.verify_buffer(O, ref, rel_tol=4e-2, abs_tol=1.5e-1, max_error_rate=0.005)
     assert not errs, f"{len(errs)} mismatches"
     assert torch.all(O.view(heads, sp, 64)[:, seq_len:].cpu() == 0)
+
+
+@pytest.mark.parametrize(
+    "H,Hkv,Sq,Skv,causal,q_offset",
+    [
+        (32, 8, 512, 512, 1, 0),  # config 5 prefill, model layout (cache of 4096 rows)
+        (32, 8, 200, 712, 1, 512),  # a second chunk: queries at positions 512..711 over the cache
+        (32, 8, 1, 4096, 1, 4095),  # one query at the last cache slot
+        (4, 2, 300, 300, 0, 0),  # not causal
+        (8, 1, 77, 130, 0, 0),  # not causal, Skv not a multiple of the 64-key block
+        (2, 2, 129, 1000, 1, 871),  # ragged query tile, long visible prefix
+    ],
+)
+def test_attention_prefill_abi(gpu, H, Hkv, Sq, Skv, causal, q_offset):
+    """iron_attention_prefill through the C ABI with the model's strided layout
+    (Q rows of H*64, a KV cache of (Hkv, max_len, 64)) against the fp32 oracle,
+    BASELINE bar: max-abs 2e-2, rel-L2 1e-2. Output rows past Sq up to out_rows
+    are zero."""
+    from iron_amd import _lib
+
+    d, max_len = 64, 4096
+    g = torch.Generator().manual_seed(H * 1000 + Sq + Skv + q_offset)
+    Q = torch.randn(Sq, H, d, generator=g).to(BF16)
+    Kc = torch.randn(Hkv, max_len, d, generator=g).to(BF16)
+    Vc = torch.randn(Hkv, max_len, d, generator=g).to(BF16)
+    out_rows = Sq + 5
+    O = torch.full((out_rows, H, d), float("nan"), dtype=BF16, device=gpu)
+    Qd, Kd, Vd = Q.to(gpu), Kc.to(gpu), Vc.to(gpu)
+    scale = 1.0 / math.sqrt(d)
+    _lib.call("iron_attention_prefill", Qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), O.data_ptr(), H, Hkv, Sq, Skv, d,
+              d, H * d, max_len * d, d, d, H * d, out_rows, causal, q_offset, scale, _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    ref = ops.attention_reference(Q.permute(1, 0, 2), Kc[:, :Skv], Vc[:, :Skv], causal=bool(causal), scale=scale,
+                                  q_offset=q_offset)
+    got = O[:Sq].cpu().permute(1, 0, 2)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(got, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+    assert torch.all(O[Sq:].cpu() == 0)
