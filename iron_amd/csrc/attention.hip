@@ -392,8 +392,15 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 31, hh = lane >> 5;
-  const int h = blockIdx.y, hk = h / (a.H / a.Hkv);
-  const int q0 = blockIdx.x * kFaQ;
+  // Workgroup order: x = head, y = query tile. Causal tiles run heaviest
+  // first (the last tile sees the most keys), and when H % 8 == 0 the heads
+  // are permuted so that each XCD (workgroup b runs on XCD b % 8) holds
+  // H / 8 consecutive heads, which share KV heads and so K/V blocks in its L2.
+  const int bx = blockIdx.x;
+  const int h = (a.H % 8 == 0) ? (bx % 8) * (a.H / 8) + bx / 8 : bx;
+  const int hk = h / (a.H / a.Hkv);
+  const int tile = a.causal ? static_cast<int>(gridDim.y) - 1 - static_cast<int>(blockIdx.y) : blockIdx.y;
+  const int q0 = tile * kFaQ;
   if (q0 >= a.Sq) {  // padding rows only (uniform per workgroup)
     for (int e = tid; e < kFaQ * (kD / 8); e += 256) {
       const int r = q0 + (e >> 3), ch = e & 7;
@@ -744,7 +751,8 @@ extern "C" int iron_attention_prefill(const void* q, const void* k, const void* 
                 scale * 1.4426950408889634f};
   IRON_REQUIRE(aligned16(out) && o_row_stride % 8 == 0 && o_head_stride % 8 == 0,
                "iron_attention_prefill: out rows must be 16-byte aligned");
-  dim3 grid((out_rows + kFaQ - 1) / kFaQ, n_heads), block(256);
+  IRON_REQUIRE((out_rows + kFaQ - 1) / kFaQ < 65536, "iron_attention_prefill: out_rows=%d too large", out_rows);
+  dim3 grid(n_heads, (out_rows + kFaQ - 1) / kFaQ), block(256);
   IRON_LAUNCH(attention_prefill_kernel, grid, block, 0, static_cast<hipStream_t>(stream), a);
   return check_launch("attention_prefill");
 }
