@@ -1,11 +1,12 @@
 #!/usr/bin/env python3
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--mode full|gemv|model]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--mode full|gemv|model|prefill]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
-runs only the Llama configuration. Both print the same JSON line shape.
+runs only the Llama configuration; --mode prefill only the config 5 prefill
+GEMM and the 3968-token causal attention (for kernel traces and counters).
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
@@ -413,7 +414,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "gemv", "model"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill"], default="full")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -437,6 +438,17 @@ def main() -> int:
 
     if args.mode == "model":
         out = {"metric": METRIC, "mode": "model", "extra": {"llama_cfg5": bench_model(torch, dev)}}
+        print(json.dumps(out), flush=True)
+        return 0
+    if args.mode == "prefill":
+        out = {
+            "metric": METRIC,
+            "mode": "prefill",
+            "extra": {
+                "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+                "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
+            },
+        }
         print(json.dumps(out), flush=True)
         return 0
 

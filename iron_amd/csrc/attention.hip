@@ -317,8 +317,9 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 // lanes 4j + i / 4 (j = 0..3), so lanes addressing 4 keys x 16 dims receive 16
 // dims x 4 keys. K rows keep the 16-byte chunk c at slot c ^ ((key / 2) % 8)
 // (16 rows of a ds_read_b128 on distinct banks); V rows at slot
-// c ^ (((key / 2) % 4) * 2), which separates rows r and r + 2 of a transposed
-// read (their chunk pair {c, c + 1} moves to another pair of slots).
+// c ^ (((key / 2) % 2) * 4): a transposed read serves 32 lanes per LDS pass,
+// 4 rows x 4 chunks, and this maps rows r and r + 2 to disjoint slot halves
+// (with rows r and r + 1 on opposite bank halves, all 64 banks once).
 // Online softmax in the log2 domain, fp32 statistics; output rows in
 // [Sq, out_rows) are zero-filled (the MHA operator's padding).
 // ---------------------------------------------------------------------------
@@ -377,7 +378,7 @@ __device__ __forceinline__ float fa_pair_sum(float x) {
 }
 
 __device__ __forceinline__ int fa_k_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
-__device__ __forceinline__ int fa_v_slot(int row, int chunk) { return chunk ^ (((row >> 1) & 3) << 1); }
+__device__ __forceinline__ int fa_v_slot(int row, int chunk) { return chunk ^ (((row >> 1) & 1) << 2); }
 
 // Wait until at most N of this wave's global loads are outstanding, then
 // barrier (__syncthreads would wait for all of them). The memory clobber keeps
