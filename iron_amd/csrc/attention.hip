@@ -437,7 +437,11 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   // loads 1 KiB blocks 4w..4w+3 (0-7 K, 8-15 V). Lane l lands on row
   // 8 (b % 8) + l / 8, slot l % 8 and fetches the chunk that belongs there.
   // Keys past Skv load key Skv-1: finite values whose weights are zero.
+  // Blocks are issued in order 0, 1, 2, ...: each lane keeps the source of
+  // its next row and bumps it by 64 rows per issue; only a block that runs
+  // past Skv recomputes clamped addresses.
   const uint16_t* src[4];
+  const uint16_t* next_src[4];
   long long rstride[4];
   int lrow[4];
 #pragma unroll
@@ -449,14 +453,17 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     src[j] = (is_k ? a.k + hk * a.k_hs : a.v + hk * a.v_hs) + chunk * 8;
     rstride[j] = is_k ? a.k_rs : a.v_rs;
     lrow[j] = r;
+    next_src[j] = src[j] + r * rstride[j];
   }
   auto issue = [&](int bi) {
     unsigned char* st = lds + (bi % kFaStages) * 2 * kFaBlock;
+    const bool inside = bi * kFaK + kFaK <= a.Skv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int key = min(bi * kFaK + lrow[j], a.Skv - 1);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + key * rstride[j]),
+      const uint16_t* p = inside ? next_src[j] : src[j] + min(bi * kFaK + lrow[j], a.Skv - 1) * rstride[j];
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(p),
                                        reinterpret_cast<unsigned*>(st + (wave * 4 + j) * 1024), 16, 0, 0);
+      next_src[j] += kFaK * rstride[j];
     }
   };
   // this lane's transposed-read address inside a V block: 16-lane group g
@@ -468,15 +475,15 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     const unsigned char* ks = lds + (bi % kFaStages) * 2 * kFaBlock;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) sc[b][j] = 0.f;
       const int kr = 32 * b + c;
+      fa_f32x16 acc = {};  // the first MFMA takes an inline zero accumulator
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         const fa_bf16x8 kf = __builtin_bit_cast(
             fa_bf16x8, *reinterpret_cast<const fa_u32x4*>(ks + kr * 128 + fa_k_slot(kr, 2 * kk + hh) * 16));
-        sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[b], 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], acc, 0, 0, 0);
       }
+      sc[b] = acc;
     }
   };
   auto visible = [&](int bi) { return !a.causal || bi * kFaK <= wave_last; };
@@ -553,8 +560,8 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
       // Online softmax in the log2 domain with c = scale * log2(e) > 0: the row
       // maximum is taken on the raw scores, p = 2^(s c - m) is one FMA and one
       // v_exp_f32. Only blocks that cross Skv or the causal diagonal of this
-      // wave's queries are masked, and O is rescaled only when some lane's
-      // maximum moved: the softmax VALU work, not the MFMAs, bounds this loop.
+      // wave's queries are masked. The softmax VALU work, not the MFMAs,
+      // bounds this loop.
       const float cs = a.scale_log2;
       float mx = -INFINITY;
       if (k0 + kFaK > a.Skv || (a.causal && k0 + kFaK - 1 > wave_first)) {
@@ -574,9 +581,23 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
           for (int j = 0; j < 16; j += 2) mx = fmaxf(mx, fmaxf(cur[b][j], cur[b][j + 1]));  // v_max3_f32
       }
       mx = fa_pair_max(mx);
-      const float mnew = fmaxf(m, mx * cs);
-      const float moff = (mnew == -INFINITY) ? 0.f : mnew;  // keeps 2^(-inf - moff) = 0, never NaN
-      const float alpha = __builtin_amdgcn_exp2f(m - moff);  // 0 on the first visible block
+      // Lazy rescaling: the running maximum m moves only when this block's
+      // maximum exceeds it by more than 8 (log2 units), so p = 2^(s c - m) <= 2^8
+      // stays well inside bf16/fp32 range and O is rarely rescaled. The result
+      // sum(p v) / sum(p) does not depend on which m is used.
+      const float mblk = mx * cs;
+      const bool grow = mblk > m + 8.f;  // first visible block: m = -inf
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m - mblk) : 1.f;  // 0 when m = -inf
+        m = grow ? mblk : m;
+        l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          o[0][j] *= alpha;
+          o[1][j] *= alpha;
+        }
+      }
+      const float moff = (m == -INFINITY) ? 0.f : m;  // keeps 2^(-inf - moff) = 0, never NaN
       // P^T fragments: pf[2 b + sp] element i = register 8 sp + i of s[b]
       fa_bf16x8 pf[4];
       float psum = 0.f;
@@ -594,15 +615,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
           for (int i = 0; i < 4; ++i) psum = dot2_bf16(w[i], 0x3f803f80u, psum);
           pf[2 * b + sp] = __builtin_bit_cast(fa_bf16x8, w);
         }
-      l = l * alpha + psum;
-      m = mnew;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          o[0][j] *= alpha;
-          o[1][j] *= alpha;
-        }
-      }
+      l += psum;
       // O^T += V^T P^T over the block's 64 keys, 4 k-steps of 16
 #pragma unroll
       for (int db = 0; db < 2; ++db)
