@@ -277,7 +277,9 @@ def bench_swiglu(torch, lib, tm, dev, n):
     return res
 
 
-def bench_prefill_gemm(torch, lib, tm, dev, n):
+def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False):
+    """Config 5 prefill GEMM M=512 K=2048 N=8192 (bf16 weights, or int4-g32
+    weights dequantised in the kernel's prologue)."""
     from iron_amd import _lib
 
     M, K, N = 512, 2048, 8192
@@ -286,17 +288,25 @@ def bench_prefill_gemm(torch, lib, tm, dev, n):
     W = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     stream = _lib.stream_handle(dev)
+    if int4:
+        codes = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
+        scales = torch.empty(N, K // 32, dtype=torch.bfloat16, device=dev)
+        _check(lib, lib.iron_quantize_i4g32(W.data_ptr(), codes.data_ptr(), scales.data_ptr(), N, K, stream))
 
     def launch(i):
-        _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
-                                          stream))
+        if int4:
+            _check(lib, lib.iron_gemm_i4g32_nt(A.data_ptr(), codes.data_ptr(), scales.data_ptr(), C.data_ptr(), M, N,
+                                               K, N, 0, 0, 0.0, 0.0, 1, 1, None, 0, stream))
+        else:
+            _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+                                              stream))
 
     for i in range(10):
         launch(i)
     t = tm.kernel_us(launch, n)
     tf = 2.0 * M * N * K / t / 1e6
-    return {"shape": [M, K, N], "kernel_us": round(t, 3), "TFLOP/s": round(tf, 1),
-            "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+    return {"shape": [M, K, N], "weights": "int4-g32" if int4 else "bf16", "kernel_us": round(t, 3),
+            "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
 def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
@@ -446,6 +456,7 @@ def main() -> int:
             "mode": "prefill",
             "extra": {
                 "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+                "prefill_gemm_int4_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, int4=True),
                 "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
             },
         }

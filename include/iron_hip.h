@@ -224,6 +224,22 @@ int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, int M, int N
                              int has_clamp, float clamp_lo, float clamp_hi, int splits, void* workspace,
                              long long workspace_bytes, void* stream);
 
+/* iron_gemm_bf16_nt with B given as int4-g32 weights and dequantized in the
+ * kernel's prologue (no bf16 copy of the weights): B[n][k] = bf16(q * s) with
+ * q the nibble of byte codes[n][k/2] (low nibble = even k; two's complement
+ * [-8, 7] when is_signed, else [0, 15]) and s = scales[n][k/32] (bf16); the
+ * dequantized values are bit-exact, and C is bit-identical to
+ * iron_gemm_bf16_nt on them. codes (N, K/2) 16-byte aligned, scales
+ * (N, K/32) 4-byte aligned, K % 64 == 0. splits > 1 splits K as
+ * iron_gemm_bf16_nt_splitk does (workspace of splits*M*N*4 bytes; unused
+ * when splits == 1). No reference counterpart as one operator: it is
+ * Dequant (iron/operators/dequant/op.py:20-81) feeding flm.GEMM / GEMM
+ * (iron/operators/flm/gemm/op.py:64-499, iron/operators/gemm/op.py:21-231)
+ * without the bf16 round trip through memory. */
+int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* scales, void* C, int M, int N, int K,
+                       long long ldc, int epilogue, int has_clamp, float clamp_lo, float clamp_hi, int is_signed,
+                       int splits, void* workspace, long long workspace_bytes, void* stream);
+
 /* out (cols, rows) = in (rows, cols)^T, bf16. Layout glue for GEMM's
  * row-major B (the role of iron/operators/transpose/op.py:18-120). */
 int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream);

@@ -49,6 +49,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int BK = 64;
 constexpr int kChunks = BK / 8;  // 16-byte chunks per LDS row
@@ -65,6 +66,11 @@ struct GemmArgs {
   float lo, hi;
   float* partial;  // split-K: fp32 (splits, M, N) partial sums instead of C
   int splits;      // K ranges (1 = no split)
+  // int4-g32 B (gemm_i4_kernel): codes (N, K/2), low nibble = even k; bf16
+  // scales (N, K/32); is_signed: two's-complement codes (else unsigned)
+  const uint8_t* codes;
+  const uint16_t* scales;
+  int is_signed;
 };
 
 template <int WMW_, int WNW_, int TI_, int TJ_, int NS_>
@@ -94,6 +100,66 @@ __device__ __forceinline__ int swz(int row, int chunk) { return row * kChunks + 
 template <int N>
 __device__ __forceinline__ void wait_loads_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Epilogue shared by the GEMM kernels. Split-K: raw fp32 sums straight from
+// the accumulators. Otherwise the C tile goes through LDS as bf16 [BM][BN]
+// (every wave must be done reading its last stage) for 16-byte row stores.
+template <class T>
+__device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&acc)[T::TI][T::TJ], u32x4v* smem,
+                                           int m0, int n0, int kb, int wm, int wn, int lane, int tid) {
+  constexpr int BM = T::BM, BN = T::BN, TI = T::TI, TJ = T::TJ;
+  if (a.partial) {  // split-K: raw fp32 sums straight from the accumulators
+    float* P = a.partial + static_cast<size_t>(kb) * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int gm = m0 + wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const int gn = n0 + wn * TJ * 32 + j * 32 + (lane & 31);
+          if (gm < a.M && gn < a.N) P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
+        }
+    return;
+  }
+
+  // epilogue through LDS: C tile as bf16 [BM][BN]
+  __syncthreads();  // every wave is done reading the last stage
+  uint16_t* Cs = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int col = wn * TJ * 32 + j * 32 + (lane & 31);
+        float x = acc[i][j][v];
+        if (a.epi != EPI_NONE || a.clamp) {
+          x = bf16_to_f32(f32_to_bf16(x));
+          x = apply_epilogue(x, a.epi);
+          if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
+        }
+        Cs[row * BN + col] = f32_to_bf16(x);
+      }
+  __syncthreads();
+  const bool full_n = (n0 + BN <= a.N) && (a.ldc % 8 == 0);
+#pragma unroll
+  for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
+    const int id = tid + i * T::kThreads, row = id / (BN / 8), c = id % (BN / 8);
+    const int gm = m0 + row, gn = n0 + c * 8;
+    if (gm >= a.M || gn >= a.N) continue;
+    const uint4 v = reinterpret_cast<const uint4*>(Cs)[row * (BN / 8) + c];
+    uint16_t* dst = a.C + static_cast<size_t>(gm) * a.ldc + gn;
+    if (full_n) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+      for (int q = 0; q < 8; ++q)
+        if (gn + q < a.N) dst[q] = e[q];
+    }
+  }
 }
 
 template <class T>
@@ -190,57 +256,199 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
     }
   }
 
-  if (a.partial) {  // split-K: raw fp32 sums straight from the accumulators
-    float* P = a.partial + static_cast<size_t>(kb) * a.M * a.N;
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int gm = m0 + wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          const int gn = n0 + wn * TJ * 32 + j * 32 + (lane & 31);
-          if (gm < a.M && gn < a.N) P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
-        }
-    return;
-  }
+  store_tile<T>(a, acc, smem, m0, n0, kb, wm, wn, lane, tid);
+}
 
-  // epilogue through LDS: C tile as bf16 [BM][BN]
-  __syncthreads();  // every wave is done reading the last stage
-  uint16_t* Cs = reinterpret_cast<uint16_t*>(smem);
+// ---------------------------------------------------------------------------
+// int4-g32 weights dequantized in the GEMM's prologue: C = epi(A . deq(B)^T),
+// deq(B)[n][k] = bf16(q[n][k] * s[n][k / 32]) (the product is exact in fp32,
+// rounded once to nearest-even), q two's-complement or unsigned nibbles, low
+// nibble first along K. Per step the workgroup fetches, by LDS-direct loads,
+// the A tile (as the bf16 kernel) plus the B codes (BN x 32 B) and scales
+// (BN x 4 B), then dequantizes the NEXT step's B tile once for all its waves
+// into one of two bf16 tiles (same swizzled layout as a bf16 B stage) after
+// issuing the current step's MFMAs, which read the other tile. The MFMA chain is the bf16 kernel's, so the
+// result is bit-identical to iron_gemm_bf16_nt on the dequantized weights.
+// Dequantization: (n ^ 8) (signed) or n via a byte mask, v_cvt_f32_ubyte,
+// one FMA with the scale (q*s = (q+8)*s - 8s exactly), v_cvt_pk_bf16_f32.
+template <int WMW_, int WNW_, int TI_, int TJ_, int NS_>
+struct TileI4 {
+  static constexpr int WMW = WMW_, WNW = WNW_, TI = TI_, TJ = TJ_, NS = NS_;
+  static constexpr int kWaves = WMW * WNW, kThreads = 64 * kWaves;
+  static constexpr int BM = WMW * TI * 32, BN = WNW * TJ * 32;
+  static constexpr int kABlocks = BM / 8;    // 1 KiB blocks of 8 A rows
+  static constexpr int kCBlocks = BN / 32;   // 1 KiB blocks of 32 code rows (32 B each)
+  static constexpr int kSBlocks = BN / 64;   // 256 B blocks of 64 scale pairs
+  static constexpr int kSlots = kABlocks + kCBlocks + kSBlocks;
+  static constexpr int kPerWave = (kSlots + kWaves - 1) / kWaves;  // loads per wave per step (padded)
+  // LDS (bytes): NS stages of [A | codes | scales], then 2 bf16 B tiles, then a dummy KiB
+  static constexpr int kStageBytes = BM * 128 + BN * 32 + BN * 4;
+  static constexpr int kBbfOff = NS * kStageBytes;
+  static constexpr int kDummyOff = kBbfOff + 2 * BN * 128;
+  static constexpr int kLds = kDummyOff + 1024;
+  static_assert(NS >= 3, "the next step's codes must be resident one step ahead");
+  static_assert(BN * 4 == kThreads, "one 16-weight quarter row per thread");
+  static_assert(kLds <= 160 * 1024 && BM * BN * 2 <= kLds, "LDS budget");
+};
+using TileI4S = TileI4<2, 4, 2, 1, 4>;  // 128x128, 8 waves of 64x32
+using TileI4M = TileI4<4, 2, 2, 2, 3>;  // 256x128, 8 waves of 64x64
+
+// 8 int4 codes of one 32-bit word -> 8 bf16 weights (4 words, k order).
+__device__ __forceinline__ u32x4v dequant8(uint32_t w, float s, bool is_signed) {
+  const uint32_t x = is_signed ? (w ^ 0x88888888u) : w;  // signed: n ^ 8 = q + 8
+  uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+  // hide the known-zero bits, so each byte converts with one v_cvt_f32_ubyteN
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  const float off = is_signed ? -8.f * s : 0.f;
+  float v[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    v[2 * b] = fmaf(static_cast<float>((lo >> (8 * b)) & 0xFFu), s, off);      // element 2b (low nibble)
+    v[2 * b + 1] = fmaf(static_cast<float>((hi >> (8 * b)) & 0xFFu), s, off);  // element 2b + 1
+  }
+  return u32x4v{cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]), cvt_pk_bf16(v[4], v[5]), cvt_pk_bf16(v[6], v[7])};
+}
+
+template <class T>
+__global__ __launch_bounds__(T::kThreads) void gemm_i4_kernel(GemmArgs a) {
+  constexpr int BM = T::BM, BN = T::BN, TI = T::TI, TJ = T::TJ, NS = T::NS, PW = T::kPerWave;
+  __shared__ u32x4v smem[T::kLds / 16];
+  unsigned char* lds = reinterpret_cast<unsigned char*>(smem);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / T::WNW, wn = wave % T::WNW;
+
+  const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+  const int nt = tiles_m * tiles_n * a.splits;
+  int t = blockIdx.x;
+  if (nt % 8 == 0) t = (t % 8) * (nt / 8) + t / 8;
+  const int kb = t / (tiles_m * tiles_n);
+  t %= tiles_m * tiles_n;
+  const int tm = t % tiles_m, tn = t / tiles_m;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = a.K / BK / a.splits;
+  const int step0 = kb * nk;  // first K step of this workgroup's range
+
+  // Load slots: A blocks, then code blocks, then scale blocks, then dummies
+  // (every wave issues exactly PW loads per step, so one vmcnt count fits all).
+  const unsigned char* src[PW];
+  int dst[PW], kind[PW];  // kind: 0 A (16 B/lane, +128 B per step), 1 codes (16 B, +32 B), 2 scales (4 B, +4 B), 3 dummy
+#pragma unroll
+  for (int j = 0; j < PW; ++j) {
+    const int slot = wave * PW + j;
+    if (slot < T::kABlocks) {
+      const int row = slot * 8 + (lane >> 3), chunk = (lane & 7) ^ ((row >> 1) & 7);
+      src[j] = reinterpret_cast<const unsigned char*>(a.A + static_cast<size_t>(min(m0 + row, a.M - 1)) * a.K +
+                                                      static_cast<size_t>(step0) * BK + chunk * 8);
+      dst[j] = slot * 1024;
+      kind[j] = 0;
+    } else if (slot < T::kABlocks + T::kCBlocks) {
+      const int c = slot - T::kABlocks, row = c * 32 + (lane >> 1);
+      src[j] = a.codes + static_cast<size_t>(min(n0 + row, a.N - 1)) * (a.K / 2) + static_cast<size_t>(step0) * 32 +
+               (lane & 1) * 16;
+      dst[j] = BM * 128 + c * 1024;
+      kind[j] = 1;
+    } else if (slot < T::kSlots) {
+      const int c = slot - T::kABlocks - T::kCBlocks, row = c * 64 + lane;
+      src[j] = reinterpret_cast<const unsigned char*>(a.scales + static_cast<size_t>(min(n0 + row, a.N - 1)) *
+                                                                    (a.K / 32) + static_cast<size_t>(step0) * 2);
+      dst[j] = BM * 128 + BN * 32 + c * 256;
+      kind[j] = 2;
+    } else {
+      src[j] = reinterpret_cast<const unsigned char*>(a.A) + (lane & 7) * 16;  // first 128 B of A (K >= 64)
+      dst[j] = 0;
+      kind[j] = 3;
+    }
+  }
+  auto issue = [&](int step) {
+    unsigned char* st = lds + (step % NS) * T::kStageBytes;
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+      if (kind[j] == 2)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + step * 4),
+                                         reinterpret_cast<unsigned*>(st + dst[j]), 4, 0, 0);
+      else if (kind[j] == 3)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j]),
+                                         reinterpret_cast<unsigned*>(lds + T::kDummyOff), 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + step * (kind[j] == 0 ? 128 : 32)),
+                                         reinterpret_cast<unsigned*>(st + dst[j]), 16, 0, 0);
+    }
+  };
+  // Thread -> quarter row of the B tile: row tid / 4, k 16 (tid % 4) .. + 16.
+  const int dq_row = tid >> 2, dq_q = tid & 3;
+  // The code and scale reads are inline assembly with their own lgkmcnt wait:
+  // as plain loads, the compiler made them wait vmcnt(0) for every LDS-direct
+  // load in flight (it cannot tell the stages apart).
+  auto dequant = [&](int step) {
+    const unsigned st = static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)) + (step % NS) * T::kStageBytes;
+    const unsigned ca = st + BM * 128 + dq_row * 32 + dq_q * 8;
+    const unsigned sa = st + BM * 128 + BN * 32 + dq_row * 4 + (dq_q >> 1) * 2;
+    u32x2v w;
+    unsigned s16;
+    asm volatile("ds_read_b64 %0, %2\n\tds_read_u16 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+                 : "=&v"(w), "=&v"(s16)
+                 : "v"(ca), "v"(sa));
+    const float sc = __builtin_bit_cast(float, s16 << 16);
+    u32x4v* bt = reinterpret_cast<u32x4v*>(lds + T::kBbfOff + (step & 1) * BN * 128);
+    bt[swz(dq_row, 2 * dq_q)] = dequant8(w.x, sc, a.is_signed);
+    bt[swz(dq_row, 2 * dq_q + 1)] = dequant8(w.y, sc, a.is_signed);
+  };
+
+  f32x16_t acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
     for (int j = 0; j < TJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int col = wn * TJ * 32 + j * 32 + (lane & 31);
-        float x = acc[i][j][v];
-        if (a.epi != EPI_NONE || a.clamp) {
-          x = bf16_to_f32(f32_to_bf16(x));
-          x = apply_epilogue(x, a.epi);
-          if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
-        }
-        Cs[row * BN + col] = f32_to_bf16(x);
-      }
-  __syncthreads();
-  const bool full_n = (n0 + BN <= a.N) && (a.ldc % 8 == 0);
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // prologue: steps 0..NS-2 in flight; step 0 resident; its B tile dequantized
 #pragma unroll
-  for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
-    const int id = tid + i * T::kThreads, row = id / (BN / 8), c = id % (BN / 8);
-    const int gm = m0 + row, gn = n0 + c * 8;
-    if (gm >= a.M || gn >= a.N) continue;
-    const uint4 v = reinterpret_cast<const uint4*>(Cs)[row * (BN / 8) + c];
-    uint16_t* dst = a.C + static_cast<size_t>(gm) * a.ldc + gn;
-    if (full_n) {
-      *reinterpret_cast<uint4*>(dst) = v;
-    } else {
-      const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
-      for (int q = 0; q < 8; ++q)
-        if (gn + q < a.N) dst[q] = e[q];
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < nk) issue(p);
+  if (NS - 1 < nk)
+    wait_loads_barrier<PW * (NS - 2)>();
+  else
+    wait_loads_barrier<0>();
+  dequant(0);
+
+  for (int s = 0; s < nk; ++s) {
+    // step s+1 resident (steps s+2..min(s+NS-2, nk-1) may stay in flight); the
+    // barrier also publishes the B tile of step s and retires every read of
+    // the stage and B tile used by step s-1
+    if (s + NS - 2 < nk)
+      wait_loads_barrier<PW * (NS - 3)>();
+    else
+      wait_loads_barrier<0>();
+    if (s + NS - 1 < nk) issue(s + NS - 1);
+    const u32x4v* As = reinterpret_cast<const u32x4v*>(lds + (s % NS) * T::kStageBytes);
+    const u32x4v* Bs = reinterpret_cast<const u32x4v*>(lds + T::kBbfOff + (s & 1) * BN * 128);
+    bf16x8_t fa[2][TI], fb[2][TJ];
+    auto frags = [&](int set, int kk) {
+      const int c = kk * 2 + (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+        fa[set][i] = __builtin_bit_cast(bf16x8_t, As[swz(wm * TI * 32 + i * 32 + (lane & 31), c)]);
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[swz(wn * TJ * 32 + j * 32 + (lane & 31), c)]);
+    };
+    frags(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int cur = kk & 1, nxt = cur ^ 1;
+      if (kk + 1 < BK / 16) frags(nxt, kk + 1);
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
     }
+    // the next step's B tile, dequantized while this step's MFMAs execute
+    if (s + 1 < nk) dequant(s + 1);
   }
+  store_tile<T>(a, acc, smem, m0, n0, kb, wm, wn, lane, tid);
 }
 
 // Split-K merge: C = clamp(act(bf16(sum_kb partial[kb]))), the same epilogue
@@ -316,6 +524,11 @@ static void launch_tile(const GemmArgs& a, hipStream_t s) {
   IRON_LAUNCH(gemm_nt_kernel<T>, dim3(static_cast<unsigned>(tile_count<T>(a))), dim3(T::kThreads), 0, s, a);
 }
 
+template <class T>
+static void launch_tile_i4(const GemmArgs& a, hipStream_t s) {
+  IRON_LAUNCH(gemm_i4_kernel<T>, dim3(static_cast<unsigned>(tile_count<T>(a))), dim3(T::kThreads), 0, s, a);
+}
+
 static void gemm_launch(const GemmArgs& a, hipStream_t s) {
   const double cl = launch_cost<TileL>(a, 1, 1000.0), cm = launch_cost<TileM>(a, 1, 900.0);
   const double cs = launch_cost<TileS>(a, 1, 660.0), cs2 = launch_cost<TileS2>(a, 2, 800.0);
@@ -381,6 +594,49 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
   const long long mn = static_cast<long long>(M) * N;
   IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
   return check_launch("gemm_bf16_nt_splitk");
+}
+
+// Cost model for the int4 kernels (measured full-occupancy rates, TFLOP/s).
+static void gemm_i4_launch(const GemmArgs& a, hipStream_t s) {
+  const double cs = launch_cost<TileI4S>(a, 1, 600.0), cm = launch_cost<TileI4M>(a, 1, 800.0);
+  if (cs <= cm)
+    launch_tile_i4<TileI4S>(a, s);
+  else
+    launch_tile_i4<TileI4M>(a, s);
+}
+
+extern "C" int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* scales, void* C, int M, int N, int K,
+                                  long long ldc, int epilogue, int has_clamp, float clamp_lo, float clamp_hi,
+                                  int is_signed, int splits, void* workspace, long long workspace_bytes,
+                                  void* stream) {
+  if (int rc = gemm_check("iron_gemm_i4g32_nt", A, codes, C, M, N, K, ldc, epilogue, has_clamp, clamp_lo, clamp_hi))
+    return rc;
+  IRON_REQUIRE(scales && (reinterpret_cast<uintptr_t>(scales) & 3u) == 0,
+               "iron_gemm_i4g32_nt: scales must be non-null and 4-byte aligned");
+  IRON_REQUIRE(splits >= 1 && (K / BK) % splits == 0,
+               "iron_gemm_i4g32_nt: splits=%d must divide the %d K steps of 64", splits, K / BK);
+  const long long tiles =
+      static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile) * splits;
+  IRON_REQUIRE(tiles < (1LL << 31) && static_cast<long long>(M) * N < (1LL << 38),
+               "iron_gemm_i4g32_nt: problem too large");
+  float* partial = nullptr;
+  if (splits > 1) {
+    const long long need = static_cast<long long>(splits) * M * N * 4;
+    IRON_REQUIRE(workspace && workspace_bytes >= need, "iron_gemm_i4g32_nt: workspace of %lld bytes < %lld",
+                 workspace_bytes, need);
+    IRON_REQUIRE(aligned16(workspace), "iron_gemm_i4g32_nt: workspace must be 16-byte aligned");
+    partial = static_cast<float*>(workspace);
+  }
+  GemmArgs a{static_cast<const uint16_t*>(A), nullptr, static_cast<uint16_t*>(C), M, N, K, ldc, epilogue, has_clamp,
+             clamp_lo, clamp_hi, partial, splits, static_cast<const uint8_t*>(codes),
+             static_cast<const uint16_t*>(scales), is_signed ? 1 : 0};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  gemm_i4_launch(a, s);
+  if (splits > 1) {
+    const long long mn = static_cast<long long>(M) * N;
+    IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
+  }
+  return check_launch("gemm_i4g32_nt");
 }
 
 extern "C" int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream) {

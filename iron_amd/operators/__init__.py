@@ -12,6 +12,7 @@ _OPERATOR_MODULES = {
     "ElementwiseAdd": "elementwise_add",
     "ElementwiseMul": "elementwise_mul",
     "GEMM": "gemm",
+    "GEMMInt4": "gemm_int4",
     "GEMV": "gemv",
     "GEMVInt4": "gemv_int4",
     "GQADecode": "gqa_decode",

@@ -176,3 +176,85 @@ def test_gemm_splitk_choice_and_errors(gpu):
     with pytest.raises(_lib.IronHipError, match="workspace"):
         _lib.call("iron_gemm_bf16_nt_splitk", A.data_ptr(), A.data_ptr(), C.data_ptr(), 128, 128, 192, 128, 0, 0,
                   0.0, 0.0, 3, C.data_ptr(), 16, _lib.stream_handle(gpu))
+
+
+@pytest.mark.parametrize(
+    "M,K,N,signed",
+    [
+        (512, 2048, 8192, True),  # config 5 gate/up shape: 128x128 tiles, one per CU
+        (512, 2048, 3072, True),  # qkv
+        (512, 2048, 2048, True),  # o_proj: split K (64 tiles)
+        (512, 8192, 2048, True),  # down_proj: split K
+        (3968, 2048, 3072, True),  # long prompt: 256x128 tiles
+        (200, 320, 1000, False),  # ragged M and N, unsigned codes
+        (1, 64, 64, True),  # smallest shape
+    ],
+)
+def test_gemm_i4g32_matches_bf16_on_dequantized(gpu, M, K, N, signed):
+    """iron_gemm_i4g32_nt dequantizes in its prologue: the result must be
+    bit-identical to iron_gemm_bf16_nt on the oracle's dequantized weights
+    (bf16(q*s), bit-exact) with the same split count, and within one bf16 ulp
+    of the fp32-accumulated product."""
+    from iron_amd import _lib
+
+    gen = torch.Generator().manual_seed(M + K + N + int(signed))
+    lo, hi = (-8, 8) if signed else (0, 16)
+    q = torch.randint(lo, hi, (N, K), generator=gen, dtype=torch.int16)
+    codes = ops.pack_int4(q)
+    scales = (0.001 + 0.009 * torch.rand(N, K // 32, generator=gen)).to(BF16)
+    A = torch.randn(M, K, generator=gen).to(BF16)
+    W = ops.dequant_planar(codes, scales, signed=signed)
+    s = _lib.stream_handle(gpu)
+    splits = _lib.query("iron_gemm_splitk_choose", M, N, K)
+    need = int(_lib.query("iron_gemm_splitk_workspace_bytes", M, N, splits))
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device=gpu)
+    Ad, Wd, cd, sd = A.to(gpu), W.to(gpu), codes.to(gpu), scales.to(gpu)
+    C4 = torch.full((M, N), float("nan"), dtype=BF16, device=gpu)
+    Cb = torch.empty(M, N, dtype=BF16, device=gpu)
+    _lib.call("iron_gemm_i4g32_nt", Ad.data_ptr(), cd.data_ptr(), sd.data_ptr(), C4.data_ptr(), M, N, K, N, 0, 0,
+              0.0, 0.0, int(signed), splits, ws.data_ptr(), need, s)
+    if splits > 1:
+        _lib.call("iron_gemm_bf16_nt_splitk", Ad.data_ptr(), Wd.data_ptr(), Cb.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+                  splits, ws.data_ptr(), need, s)
+    else:
+        _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), Cb.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0, s)
+    torch.cuda.synchronize()
+    assert torch.equal(C4.cpu().view(torch.int16), Cb.cpu().view(torch.int16))
+    ref = A.float() @ W.float().T
+    bad = ops.within_bf16_ulps(C4, ref, n_ulp=1.0, atol=1e-5 * float(ref.abs().max()))
+    assert not bad, bad[:5]
+
+
+def test_gemm_int4_operator_epilogue_and_errors(gpu):
+    """GEMMInt4 operator (arg order A, codes, scales, C) against GEMM on the
+    dequantized weights; the flm epilogue path of the C ABI; argument checks."""
+    from iron_amd import _lib
+    from iron_amd.operators import GEMM, GEMMInt4
+
+    M, K, N = 256, 1024, 768
+    gen = torch.Generator().manual_seed(7)
+    q = torch.randint(-8, 8, (N, K), generator=gen, dtype=torch.int16)
+    codes, scales = ops.pack_int4(q), (0.001 + 0.009 * torch.rand(N, K // 32, generator=gen)).to(BF16)
+    A = torch.randn(M, K, generator=gen).to(BF16)
+    W = ops.dequant_planar(codes, scales)
+    Ad, Wd, cd, sd = A.to(gpu), W.to(gpu), codes.to(gpu), scales.to(gpu)
+    C4 = torch.empty(M, N, dtype=BF16, device=gpu)
+    Cb = torch.empty(M, N, dtype=BF16, device=gpu)
+    GEMMInt4(M=M, K=K, N=N).get_callable()(Ad, cd, sd, C4)
+    GEMM(M=M, K=K, N=N, b_col_maj=True).get_callable()(Ad, Wd, Cb)
+    torch.cuda.synchronize()
+    assert torch.equal(C4.cpu().view(torch.int16), Cb.cpu().view(torch.int16))
+    s = _lib.stream_handle(gpu)
+    _lib.call("iron_gemm_i4g32_nt", Ad.data_ptr(), cd.data_ptr(), sd.data_ptr(), C4.data_ptr(), M, N, K, N, 2, 1,
+              -1.0, 1.5, 1, 1, None, 0, s)
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), Cb.data_ptr(), M, N, K, N, 2, 1, -1.0, 1.5, s)
+    torch.cuda.synchronize()
+    assert torch.equal(C4.cpu().view(torch.int16), Cb.cpu().view(torch.int16))
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.call("iron_gemm_i4g32_nt", Ad.data_ptr(), cd.data_ptr(), sd.data_ptr(), C4.data_ptr(), M, N, 96, N, 0,
+                  0, 0.0, 0.0, 1, 1, None, 0, s)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("iron_gemm_i4g32_nt", Ad.data_ptr(), cd.data_ptr(), sd.data_ptr(), C4.data_ptr(), M, N, K, N, 0, 0,
+                  0.0, 0.0, 1, 2, None, 0, s)
+    with pytest.raises(ValueError):
+        GEMMInt4(M=M, K=96, N=N)

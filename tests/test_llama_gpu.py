@@ -104,3 +104,20 @@ def test_full_size_model_teacher_forced(gpu):
     assert res[0][0] <= 0.1, res[0]
     assert all(kl <= 0.05 for kl, _ in res[1:]), res
     assert sum(t for _, t in res) >= len(res) - 1, res
+
+
+def test_prefill_from_int4_bitwise(gpu):
+    """prefill_int4=True (prefill GEMMs dequantise the int4 weights in the
+    kernel, no bf16 copies) gives bitwise the same logits and tokens as the
+    bf16-copy prefill: the dequantised values and the MFMA order are the same."""
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
+
+    outs = []
+    for prefill_int4 in (False, True):
+        cfg = LlamaConfig(prefill_int4=prefill_int4, **TINY)
+        model = LlamaHIP(cfg, random_weights(cfg, gpu, seed=6), device=gpu)
+        assert (model.layers[0]["gate"]._bf16 is None) == prefill_int4
+        toks = model.generate(list(range(7, 70)), 8)
+        outs.append((toks, model.logits.clone().view(torch.int16)))
+    assert outs[0][0] == outs[1][0]
+    assert torch.equal(outs[0][1], outs[1][1])
