@@ -224,6 +224,17 @@ int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, int M, int N
                              int has_clamp, float clamp_lo, float clamp_hi, int splits, void* workspace,
                              long long workspace_bytes, void* stream);
 
+/* Fused SwiGLU projection for prefill: H (M, F) = bf16(silu(G) * U) with
+ * G = bf16(A . Wg^T), U = bf16(A . Wu^T), one GEMM over Bgu (2F, K) whose rows
+ * alternate 64-row blocks of Wg and Wu (rows 128p..128p+63 = Wg rows
+ * 64p..64p+63, the next 64 = Wu rows 64p..). F % 64 == 0, K % 64 == 0, H row
+ * stride ldh. Bit-identical to two iron_gemm_bf16_nt calls + iron_silu_mul,
+ * without writing G and U. Replaces the gate/up GEMMs + SiLU + ElementwiseMul
+ * steps of SwiGLUPrefill (iron/operators/swiglu_prefill/op.py:13-115) and of
+ * the Llama prefill (llama_npu.py:97-274). */
+int iron_gemm_bf16_nt_swiglu(const void* A, const void* Bgu, void* H, int M, int F, int K, long long ldh,
+                             void* stream);
+
 /* iron_gemm_bf16_nt with B given as int4-g32 weights and dequantized in the
  * kernel's prologue (no bf16 copy of the weights): B[n][k] = bf16(q * s) with
  * q the nibble of byte codes[n][k/2] (low nibble = even k; two's complement

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, list] = {
     "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
     "iron_gemm_bf16_nt": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _P],
     "iron_gemm_bf16_nt_splitk": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _I, _P, _LL, _P],
+    "iron_gemm_bf16_nt_swiglu": [_P, _P, _P, _I, _I, _I, _LL, _P],
     "iron_gemm_i4g32_nt": [_P, _P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _I, _I, _P, _LL, _P],
     "iron_transpose_bf16": [_P, _P, _I, _I, _P],
     "iron_transpose_batched_bf16": [_P, _P, _I, _I, _I, _P],

@@ -242,6 +242,13 @@ class LlamaHIP:
                 "up": Linear(fold(w[p + "mlp.up_proj.weight"], fn), cfg.int4, s, keep_bf16=keep),
                 "down": Linear(w[p + "mlp.down_proj.weight"], cfg.int4, s, keep_bf16=keep),
             })
+            if keep:  # prefill SwiGLU as one GEMM over 64-row blocks alternating gate / up
+                L = self.layers[-1]
+                F, K = L["gate"].N, L["gate"].K
+                L["gate_up"] = torch.stack([L["gate"].bf16.view(F // 64, 64, K), L["up"].bf16.view(F // 64, 64, K)],
+                                           dim=1).reshape(2 * F, K).contiguous()
+                if cfg.int4:  # the decode GEMVs read the int4 codes; the separate copies are not needed
+                    L["gate"]._bf16 = L["up"]._bf16 = None
         del w
         L = cfg.max_seq_len
         self.k_cache = [torch.zeros(cfg.n_kv_groups, L, Hd, dtype=BF16, device=dev) for _ in range(cfg.n_layers)]
@@ -427,9 +434,14 @@ class LlamaHIP:
             L["o"].gemm(b["O"], T, S, s, self._workspace)
             _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
                       float(cfg.eps), s)
-            L["gate"].gemm(Xn, b["G"], S, s, self._workspace)
-            L["up"].gemm(Xn, b["U"], S, s, self._workspace)
-            _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(), S * cfg.hidden_dim, s)
+            if "gate_up" in L:  # G = silu(Xn Wg^T) * (Xn Wu^T) in one GEMM
+                _lib.call("iron_gemm_bf16_nt_swiglu", Xn.data_ptr(), L["gate_up"].data_ptr(), b["G"].data_ptr(), S,
+                          cfg.hidden_dim, E, cfg.hidden_dim, s)
+            else:
+                L["gate"].gemm(Xn, b["G"], S, s, self._workspace)
+                L["up"].gemm(Xn, b["U"], S, s, self._workspace)
+                _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(),
+                          S * cfg.hidden_dim, s)
             L["down"].gemm(b["G"], T, S, s, self._workspace)
         _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
                   float(cfg.eps), s)

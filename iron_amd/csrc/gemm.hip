@@ -54,6 +54,9 @@ typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 constexpr int BK = 64;
 constexpr int kChunks = BK / 8;  // 16-byte chunks per LDS row
 constexpr int kSplitTile = 128;  // tile edge the split-K policy counts in
+// Epilogue of the fused SwiGLU GEMM (iron_gemm_bf16_nt_swiglu); not part of the
+// public enum: B rows come in 64-row blocks alternating gate / up.
+constexpr int kEpiSwigluPair = 100;
 
 struct GemmArgs {
   const uint16_t* A;  // (M, K)
@@ -127,6 +130,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
   // epilogue through LDS: C tile as bf16 [BM][BN]
   __syncthreads();  // every wave is done reading the last stage
   uint16_t* Cs = reinterpret_cast<uint16_t*>(smem);
+  const bool swiglu = a.epi == kEpiSwigluPair;
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -136,7 +140,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
         const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         const int col = wn * TJ * 32 + j * 32 + (lane & 31);
         float x = acc[i][j][v];
-        if (a.epi != EPI_NONE || a.clamp) {
+        if (!swiglu && (a.epi != EPI_NONE || a.clamp)) {
           x = bf16_to_f32(f32_to_bf16(x));
           x = apply_epilogue(x, a.epi);
           if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
@@ -144,6 +148,36 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
         Cs[row * BN + col] = f32_to_bf16(x);
       }
   __syncthreads();
+  if (swiglu) {
+    // Column blocks 2p and 2p+1 of 64 hold gate and up of features
+    // n0/2 + 64p .. + 63: h = bf16(silu(g) * u) of the bf16-rounded g and u,
+    // as iron_silu_mul on separate gate and up GEMM outputs. C is (M, N/2).
+    constexpr int CH = BN / 16;  // 8-feature chunks per output row
+    const int F = a.N / 2;
+    const bool full_f = (n0 / 2 + BN / 2 <= F) && (a.ldc % 8 == 0);
+#pragma unroll
+    for (int i = 0; i < (BM * CH) / T::kThreads; ++i) {
+      const int id = tid + i * T::kThreads, row = id / CH, c = id % CH;
+      const int gcol = (c / 8) * 128 + (c % 8) * 8;
+      const int gm = m0 + row, gf = n0 / 2 + c * 8;
+      if (gm >= a.M || gf >= F) continue;
+      const uint4 gv = reinterpret_cast<const uint4*>(Cs)[(row * BN + gcol) / 8];
+      const uint4 uv = reinterpret_cast<const uint4*>(Cs)[(row * BN + gcol + 64) / 8];
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        h[e] = cvt_pk_bf16(silu_f32(lo_bf16(gw[e])) * lo_bf16(uw[e]), silu_f32(hi_bf16(gw[e])) * hi_bf16(uw[e]));
+      uint16_t* dst = a.C + static_cast<size_t>(gm) * a.ldc + gf;
+      if (full_f) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(h[0], h[1], h[2], h[3]);
+      } else {
+        for (int q = 0; q < 8; ++q)
+          if (gf + q < F) dst[q] = static_cast<uint16_t>(h[q / 2] >> (16 * (q & 1)));
+      }
+    }
+    return;
+  }
   const bool full_n = (n0 + BN <= a.N) && (a.ldc % 8 == 0);
 #pragma unroll
   for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
@@ -594,6 +628,21 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
   const long long mn = static_cast<long long>(M) * N;
   IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
   return check_launch("gemm_bf16_nt_splitk");
+}
+
+extern "C" int iron_gemm_bf16_nt_swiglu(const void* A, const void* Bgu, void* H, int M, int F, int K, long long ldh,
+                                        void* stream) {
+  IRON_REQUIRE(F > 0 && F % 64 == 0, "iron_gemm_bf16_nt_swiglu: F=%d must be a positive multiple of 64", F);
+  IRON_REQUIRE(ldh >= F, "iron_gemm_bf16_nt_swiglu: ldh=%lld < F=%d", ldh, F);
+  if (int rc = gemm_check("iron_gemm_bf16_nt_swiglu", A, Bgu, H, M, 2 * F, K, 2 * ldh, EPI_NONE, 0, 0.f, 0.f))
+    return rc;
+  IRON_REQUIRE(ldh % 8 != 0 || aligned16(H), "iron_gemm_bf16_nt_swiglu: H must be 16-byte aligned");
+  const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((2 * F) / kSplitTile);
+  IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt_swiglu: problem too large");
+  GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(Bgu), static_cast<uint16_t*>(H), M, 2 * F,
+             K, ldh, kEpiSwigluPair, 0, 0.f, 0.f, nullptr, 1};
+  gemm_launch(a, static_cast<hipStream_t>(stream));
+  return check_launch("gemm_bf16_nt_swiglu");
 }
 
 // Cost model for the int4 kernels (measured full-occupancy rates, TFLOP/s).

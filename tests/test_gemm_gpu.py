@@ -258,3 +258,38 @@ def test_gemm_int4_operator_epilogue_and_errors(gpu):
                   0.0, 0.0, 1, 2, None, 0, s)
     with pytest.raises(ValueError):
         GEMMInt4(M=M, K=96, N=N)
+
+
+def _interleave_gate_up(Wg, Wu):
+    F, K = Wg.shape
+    return torch.stack([Wg.view(F // 64, 64, K), Wu.view(F // 64, 64, K)], dim=1).reshape(2 * F, K).contiguous()
+
+
+@pytest.mark.parametrize("M,K,F", [(512, 2048, 8192), (3968, 2048, 8192), (100, 256, 320), (1, 64, 64)])
+def test_gemm_swiglu_matches_unfused(gpu, M, K, F):
+    """iron_gemm_bf16_nt_swiglu over the 64-row interleaved [gate; up] weight
+    is bit-identical to gate GEMM + up GEMM + iron_silu_mul, and within the
+    BASELINE bar of the fp32 SwiGLU."""
+    from iron_amd import _lib
+
+    gen = torch.Generator().manual_seed(M + K + F)
+    A = torch.randn(M, K, generator=gen).to(BF16)
+    Wg = (torch.randn(F, K, generator=gen) * 0.02).to(BF16)
+    Wu = (torch.randn(F, K, generator=gen) * 0.02).to(BF16)
+    Ad, Wgd, Wud = A.to(gpu), Wg.to(gpu), Wu.to(gpu)
+    Wgu = _interleave_gate_up(Wgd, Wud)
+    s = _lib.stream_handle(gpu)
+    H = torch.full((M, F), float("nan"), dtype=BF16, device=gpu)
+    G = torch.empty(M, F, dtype=BF16, device=gpu)
+    U = torch.empty(M, F, dtype=BF16, device=gpu)
+    _lib.call("iron_gemm_bf16_nt_swiglu", Ad.data_ptr(), Wgu.data_ptr(), H.data_ptr(), M, F, K, F, s)
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wgd.data_ptr(), G.data_ptr(), M, F, K, F, 0, 0, 0.0, 0.0, s)
+    _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wud.data_ptr(), U.data_ptr(), M, F, K, F, 0, 0, 0.0, 0.0, s)
+    _lib.call("iron_silu_mul", G.data_ptr(), U.data_ptr(), G.data_ptr(), M * F, s)
+    torch.cuda.synchronize()
+    assert torch.equal(H.cpu().view(torch.int16), G.cpu().view(torch.int16))
+    ref = torch.nn.functional.silu(A.float() @ Wg.float().T) * (A.float() @ Wu.float().T)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(H, ref)
+    assert rel_l2 <= 1e-2 and max_abs <= 2e-2 * max(1.0, float(ref.abs().max())), (max_abs, rel_l2)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.call("iron_gemm_bf16_nt_swiglu", Ad.data_ptr(), Wgu.data_ptr(), H.data_ptr(), M, F + 32, K, F + 32, s)

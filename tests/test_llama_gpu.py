@@ -108,15 +108,17 @@ def test_full_size_model_teacher_forced(gpu):
 
 def test_prefill_from_int4_bitwise(gpu):
     """prefill_int4=True (prefill GEMMs dequantise the int4 weights in the
-    kernel, no bf16 copies) gives bitwise the same logits and tokens as the
-    bf16-copy prefill: the dequantised values and the MFMA order are the same."""
+    kernel, no bf16 copies; separate gate/up GEMMs + SiLU*mul) gives bitwise
+    the same logits and tokens as the bf16-copy prefill (fused SwiGLU GEMM):
+    the dequantised values, the MFMA order and the epilogue arithmetic match."""
     from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
 
     outs = []
     for prefill_int4 in (False, True):
         cfg = LlamaConfig(prefill_int4=prefill_int4, **TINY)
         model = LlamaHIP(cfg, random_weights(cfg, gpu, seed=6), device=gpu)
-        assert (model.layers[0]["gate"]._bf16 is None) == prefill_int4
+        assert (model.layers[0]["qkv"]._bf16 is None) == prefill_int4
+        assert ("gate_up" in model.layers[0]) != prefill_int4  # fused SwiGLU GEMM on the bf16 path
         toks = model.generate(list(range(7, 70)), 8)
         outs.append((toks, model.logits.clone().view(torch.int16)))
     assert outs[0][0] == outs[1][0]
