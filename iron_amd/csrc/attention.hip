@@ -103,26 +103,19 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   const bool lower = c < 4;
   const bool owner = pos >= p0 && pos < p0 + kDecChunk;
 
+  // Cache rows of the chunk: unconditional loads of a clamped row (a guarded
+  // load compiled to a branch waiting for its data); rows >= pos are replaced
+  // below (the new token) or masked (past it).
   uint4 kraw[2], vraw[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int p = p0 + r + 32 * h;
-    kraw[h] = vraw[h] = make_uint4(0, 0, 0, 0);
-    if (p < pos) {
-      const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
-      kraw[h] = ld_stream16(a.k_cache + off);
-      vraw[h] = ld_stream16(a.v_cache + off);
-    }
+    const int p = min(p0 + r + 32 * h, a.max_len - 1);
+    const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
+    kraw[h] = ld_stream16(a.k_cache + off);
+    vraw[h] = ld_stream16(a.v_cache + off);
   }
-  // q rotated once per workgroup: thread t -> element (t / 64, t % 64) into LDS
-  const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
   const float* angrow = a.angles + static_cast<size_t>(pos) * D;
-  for (int t = tid; t < G * D; t += kDecThreads) {
-    const int d = t % D, i = d & 31;
-    const float x = bf16_to_f32(qh[t]), xp = bf16_to_f32(qh[t ^ 32]);
-    const float cs = angrow[2 * i], sn = angrow[2 * i + 1];
-    q_s[t / D][d] = bf16_to_f32(f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn));
-  }
+  // the owner's table row and new k/v, in flight with the cache rows
   float ang[16];
   uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
   if (owner) {
@@ -138,6 +131,14 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + c * 8);
     knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (c ^ 4) * 8);
     vn = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + c * 8);
+  }
+  // q rotated once per workgroup: thread t -> element (t / 64, t % 64) into LDS
+  const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
+  for (int t = tid; t < G * D; t += kDecThreads) {
+    const int d = t % D, i = d & 31;
+    const float x = bf16_to_f32(qh[t]), xp = bf16_to_f32(qh[t ^ 32]);
+    const float cs = angrow[2 * i], sn = angrow[2 * i + 1];
+    q_s[t / D][d] = bf16_to_f32(f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn));
   }
   __syncthreads();
   float qv[G][8];
@@ -166,6 +167,11 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     } else {
       unpack8(kraw[h], kf[h]);
       unpack8(vraw[h], vf[h]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {  // rows past pos hold stale cache data: 0 * NaN must not reach o
+        kf[h][e] = valid[h] ? kf[h][e] : 0.f;
+        vf[h][e] = valid[h] ? vf[h][e] : 0.f;
+      }
     }
   }
 
@@ -246,24 +252,40 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
   __shared__ float m_s[kMergeThreads], l_s[kMergeThreads], o_s[kMergeThreads];
   const int tid = threadIdx.x, t = tid % NT, q = tid / NT, g = t / D;
   const int j = blockIdx.x;
+  const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
+  // The first B chunks of this slice are loaded before the position is known
+  // (any chunk < nsplit is inside the workspace); chunks past the active count
+  // are dropped by selects below, so stale workspace values never mix in.
+  // (Unconditional loads of a clamped chunk index: a guarded load compiled to
+  // a branch that waited for its data before the next chunk's loads.)
+  float mb[B], lb[B], ob[B];
+#pragma unroll
+  for (int b = 0; b < B; ++b) {
+    const float* pk = base + static_cast<size_t>(min(q + b * NQ, a.nsplit - 1)) * PS;
+    mb[b] = pk[G * D + g];
+    lb[b] = pk[G * D + G + g];
+    ob[b] = pk[t];
+  }
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
   const int nact = (pos + kDecChunk) / kDecChunk;
-  const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
   float M = -INFINITY, Ls = 0.f, acc = 0.f;
   for (int k0 = q; k0 < nact; k0 += NQ * B) {
-    float mb[B], lb[B], ob[B];
+    if (k0 != q) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int k = k0 + b * NQ;
-      mb[b] = -INFINITY;
-      lb[b] = ob[b] = 0.f;
-      if (k < nact) {
-        const float* pk = base + static_cast<size_t>(k) * PS;
+      for (int b = 0; b < B; ++b) {
+        const float* pk = base + static_cast<size_t>(min(k0 + b * NQ, nact - 1)) * PS;
         mb[b] = pk[G * D + g];
         lb[b] = pk[G * D + G + g];
         ob[b] = pk[t];
       }
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {  // chunks past the active count (or stale ones) weigh nothing
+      const bool live = k0 + b * NQ < nact;
+      mb[b] = live ? mb[b] : -INFINITY;
+      lb[b] = live ? lb[b] : 0.f;
+      ob[b] = live ? ob[b] : 0.f;
     }
     float bm = M;
 #pragma unroll

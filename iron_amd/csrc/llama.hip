@@ -83,16 +83,16 @@ __global__ __launch_bounds__(1024) void select_embed_kernel(const unsigned long 
   __shared__ unsigned long long ks[16];
   __shared__ int tok_s;
   const int p = pos ? *pos : 0;  // independent of the keys: in flight with them
-  // 16 keys per thread per step, all loads issued before the first compare
-  constexpr int U = 16;
+  // 32 keys per thread per step, all loads issued before the first compare
+  // (one step covers the 32064 keys of a 128256-row head)
+  constexpr int U = 32;
   unsigned long long best = 0;
   for (int base = 0; base < n_keys; base += 1024 * U) {
     unsigned long long k[U];
+    // unconditional loads of a clamped index (a repeated key cannot change the
+    // maximum): a guarded load became a branch with its own wait per key
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = base + u * 1024 + static_cast<int>(threadIdx.x);
-      k[u] = i < n_keys ? keys[i] : 0ull;
-    }
+    for (int u = 0; u < U; ++u) k[u] = keys[min(base + u * 1024 + static_cast<int>(threadIdx.x), n_keys - 1)];
 #pragma unroll
     for (int u = 0; u < U; ++u) best = k[u] > best ? k[u] : best;
   }
