@@ -52,7 +52,7 @@ METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE +
 # WRITE_SIZE, each scaled by the counter's reading for a copy of known size
 # (profiles/gemv_i4g32_cfg2_pmc.md).
-TRAFFIC_BYTES = 9553288
+TRAFFIC_BYTES = 9541893
 
 
 class Timer:
