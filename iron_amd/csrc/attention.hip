@@ -235,23 +235,23 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   }
 }
 
-// Merge of the chunk partials of one KV head, one 1024-thread workgroup per
-// KV head. Thread -> output element t = (head, dim) of the G*64 outputs and
-// slice q of the chunks (chunks q, q + NQ, ...). Each thread folds its chunks
-// with a running maximum, loading 8 chunks per step with every load in
-// flight; the NQ slices are then combined through LDS.
+// Merge of the chunk partials, one 1024-thread workgroup per query head
+// (Hkv * G workgroups). Thread -> output dim d of the head and slice q of the
+// chunks (chunks q, q + 16, ...). Each thread folds its chunks with a running
+// maximum, loading 8 chunks per step with every load in flight (one step
+// covers 128 chunks, i.e. 8192 positions); the 16 slices are then combined
+// through LDS.
 constexpr int kMergeThreads = 1024;
 
 template <int G>
 __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int PS = part_stride<G>();
-  constexpr int NT = G * D;                   // outputs per KV head
-  constexpr int NQ = kMergeThreads / NT;      // chunk slices
-  constexpr int B = 8;                        // chunks per step per thread
+  constexpr int NQ = kMergeThreads / D;  // chunk slices
+  constexpr int B = 8;                   // chunks per step per thread
   __shared__ float m_s[kMergeThreads], l_s[kMergeThreads], o_s[kMergeThreads];
-  const int tid = threadIdx.x, t = tid % NT, q = tid / NT, g = t / D;
-  const int j = blockIdx.x;
+  const int tid = threadIdx.x, d = tid % D, q = tid / D;
+  const int h = blockIdx.x, j = h / G, g = h % G;
   const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
   // The first B chunks of this slice are loaded before the position is known
   // (any chunk < nsplit is inside the workspace); chunks past the active count
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
     const float* pk = base + static_cast<size_t>(min(q + b * NQ, a.nsplit - 1)) * PS;
     mb[b] = pk[G * D + g];
     lb[b] = pk[G * D + G + g];
-    ob[b] = pk[t];
+    ob[b] = pk[g * D + d];
   }
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
         const float* pk = base + static_cast<size_t>(min(k0 + b * NQ, nact - 1)) * PS;
         mb[b] = pk[G * D + g];
         lb[b] = pk[G * D + G + g];
-        ob[b] = pk[t];
+        ob[b] = pk[g * D + d];
       }
     }
 #pragma unroll
@@ -308,15 +308,15 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
   if (q == 0) {
     float Mx = M;  // slice 0 always holds chunk 0
 #pragma unroll
-    for (int qq = 1; qq < NQ; ++qq) Mx = fmaxf(Mx, m_s[qq * NT + t]);
+    for (int qq = 1; qq < NQ; ++qq) Mx = fmaxf(Mx, m_s[qq * D + d]);
     float lt = 0.f, ot = 0.f;
 #pragma unroll
     for (int qq = 0; qq < NQ; ++qq) {
-      const float w = exp2f(m_s[qq * NT + t] - Mx);  // 0 for an empty slice
-      lt = fmaf(w, l_s[qq * NT + t], lt);
-      ot = fmaf(w, o_s[qq * NT + t], ot);
+      const float w = exp2f(m_s[qq * D + d] - Mx);  // 0 for an empty slice
+      lt = fmaf(w, l_s[qq * D + d], lt);
+      ot = fmaf(w, o_s[qq * D + d], ot);
     }
-    a.out[static_cast<size_t>(j) * NT + t] = f32_to_bf16(ot / lt);
+    a.out[static_cast<size_t>(h) * D + d] = f32_to_bf16(ot / lt);
   }
 }
 
@@ -726,7 +726,7 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
   a.scale_log2 = scale * 1.4426950408889634f;
   dim3 grid(a.nsplit, n_kv_heads), block(kDecThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 cgrid(n_kv_heads), cblock(kMergeThreads);
+  dim3 cgrid(n_kv_heads * G), cblock(kMergeThreads);
   switch (G) {
     case 1:
       IRON_LAUNCH((gqa_decode_kernel<1>), grid, block, 0, s, a);
