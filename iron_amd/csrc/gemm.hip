@@ -270,6 +270,11 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
   for (int s = 0; s < nk; ++s) {
     // the stage read in step s-1: every wave passed the barrier after its last read of it
     if (s + NS - 1 < nk) issue(s + NS - 1);
+    // The compiler waits for every outstanding LDS read (lgkmcnt(0)) before each
+    // k-slice's MFMAs, so how it interleaves the next slice's fragment reads with
+    // this slice's MFMAs sets how much LDS latency is exposed; its DS/MFMA
+    // interleave strategy 0 measured 2-4% faster on every shape than its default.
+    __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int cur = kk & 1, nxt = cur ^ 1;
@@ -469,6 +474,7 @@ __global__ __launch_bounds__(T::kThreads) void gemm_i4_kernel(GemmArgs a) {
         fb[set][j] = __builtin_bit_cast(bf16x8_t, Bs[swz(wn * TJ * 32 + j * 32 + (lane & 31), c)]);
     };
     frags(0, 0);
+    __builtin_amdgcn_iglp_opt(0);  // as in gemm_nt_kernel: 2.6-3.5% faster
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int cur = kk & 1, nxt = cur ^ 1;
