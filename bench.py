@@ -380,6 +380,28 @@ def bench_model(torch, dev, decode_steps=128, prompt_len=512, long_ctx=3968):
     out["decode_bytes_per_token_kv4096"] = int(per_tok)
     out["decode_GB/s_kv3968_4096"] = round(per_tok * out["decode_tok_s_kv3968_4096"] / 1e9, 1)
     out["decode_frac_hbm_kv3968_4096"] = round(out["decode_GB/s_kv3968_4096"] / HBM_PEAK_GBS, 4)
+
+    # the same window with LlamaConfig(head_int4=True): the tied head as int4-g32 too
+    del model
+    torch.cuda.empty_cache()
+    cfg4 = LlamaConfig(max_seq_len=long_ctx + decode_steps + 64, head_int4=True)
+    model = LlamaHIP(cfg4, random_weights(cfg4, dev, seed=0), device=dev)
+    model.reset()
+    model.prefill(prompt)
+    model.capture_decode_graph()
+    model.reset()
+    model.prefill(long_prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.decode(decode_steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    head4 = V * E // 2 + V * (E // 32) * 2
+    out["int4_head"] = {
+        "decode_tok_s_kv3968_4096": round(decode_steps / dt, 1),
+        "decode_ms_per_token_kv3968_4096": round(dt / decode_steps * 1e3, 4),
+        "decode_bytes_per_token_kv4096": int(lin + kv + head4),
+    }
     return out
 
 

@@ -93,17 +93,25 @@ __device__ __forceinline__ float finish_row(bool has_resid, float rv, int epi, u
   return bf16_to_f32(o);
 }
 
-// Workgroup argmax of the rows its waves produced: keys[key_idx] = best key.
+// Workgroup argmax of the rows its waves produced, one key per 4 rows: with R
+// rows per wave, waves 4/R*g .. 4/R*g + 4/R - 1 form key g of the workgroup,
+// written to keys[key_idx * R + g] when that index is below n_keys.
 // Every wave of the workgroup must call it (inactive waves pass key 0).
-__device__ __forceinline__ void publish_key(unsigned long long* keys, size_t key_idx, unsigned long long key) {
+template <int R = 1>
+__device__ __forceinline__ void publish_key(unsigned long long* keys, size_t key_idx, unsigned long long key,
+                                            size_t n_keys = ~size_t(0)) {
+  static_assert(R == 1 || R == 2 || R == 4, "4 rows per key");
+  constexpr int WPK = 4 / R;  // waves per key
   __shared__ unsigned long long ks[4];
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & (kWave - 1)) == 0) ks[wave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long b = ks[0];
-    for (int w = 1; w < 4; ++w) b = ks[w] > b ? ks[w] : b;
-    keys[key_idx] = b;
+  if (threadIdx.x < R) {
+    const int g = threadIdx.x;
+    unsigned long long b = ks[g * WPK];
+    for (int w = 1; w < WPK; ++w) b = ks[g * WPK + w] > b ? ks[g * WPK + w] : b;
+    const size_t idx = key_idx * R + g;
+    if (idx < n_keys) keys[idx] = b;
   }
 }
 
@@ -281,7 +289,7 @@ struct I4Args {
   uint16_t* y;
   const uint16_t* norm_w;
   const uint16_t* resid;
-  unsigned long long* keys;  // optional argmax key per workgroup (4 rows; R forced to 1)
+  unsigned long long* keys;  // optional argmax key per 4 rows (R rows per wave: R keys per workgroup)
   int M, K;
   float eps;
   int epi;
@@ -486,7 +494,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       }
     }
   }
-  if (KS == 1 && a.keys) publish_key(a.keys, tile, key);
+  if (KS == 1 && a.keys) publish_key<R>(a.keys, tile, key, (static_cast<size_t>(a.M) + 3) / 4);
 }
 
 // Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
@@ -553,9 +561,12 @@ void launch_i4_fast(const I4Args& a, int norm_mode, hipStream_t s) {
 
 template <bool PAIR>
 int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
-  // Argmax keys are defined per 4 rows: one row per wave, no K split.
+  // Argmax keys are defined per 4 rows: no K split; two rows per wave (two keys
+  // per workgroup) for the long lm_head, where one row per wave made the launch
+  // VALU-bound (128256x2048: 46 us against 31 us without keys).
   if (a.keys) {
-    if (a.K == 2048) launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
+    if (a.K == 2048 && a.M % 2 == 0 && a.M >= 8192) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
+    else if (a.K == 2048) launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
     else IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
     return check_launch("gemv_i4g32");
   }

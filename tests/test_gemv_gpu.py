@@ -228,7 +228,7 @@ def test_config4_swiglu_block(gpu, int4, mode):
 
 
 @pytest.mark.parametrize("int4", [False, True])
-@pytest.mark.parametrize("M", [1000, 128256])
+@pytest.mark.parametrize("M", [1000, 8194, 8196, 128256])
 def test_argmax_keys_and_select(gpu, int4, M):
     """GEMV argmax keys + iron_argmax_select == torch.argmax of the GEMV's own
     bf16 output (first index on ties); the selected row is embedded."""

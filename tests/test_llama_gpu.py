@@ -48,6 +48,19 @@ def _teacher_forced(model, ref, prompt, steps, use_graph):
     return results
 
 
+def test_tiny_model_int4_head(gpu):
+    """LlamaConfig(head_int4=True): the tied head quantized to int4-g32 (the
+    oracle gets the same dequantised head), same accuracy gate."""
+    model, ref = _models(gpu, seed=5, head_int4=True, **TINY)
+    assert model.head.int4 and model.head.codes is not None
+    g = torch.Generator().manual_seed(6)
+    prompt = torch.randint(0, 1000, (29,), generator=g).tolist()
+    res = _teacher_forced(model, ref, prompt, steps=8, use_graph=True)
+    assert res[0][0] <= 0.1, res[0]
+    assert all(kl <= 0.05 for kl, _ in res[1:]), res
+    assert sum(t for _, t in res) >= len(res) - 1, res
+
+
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_tiny_model_teacher_forced(gpu, use_graph):
     model, ref = _models(gpu, seed=1, **TINY)
