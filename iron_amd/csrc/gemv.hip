@@ -561,11 +561,14 @@ void launch_i4_fast(const I4Args& a, int norm_mode, hipStream_t s) {
 
 template <bool PAIR>
 int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
-  // Argmax keys are defined per 4 rows: no K split; two rows per wave (two keys
-  // per workgroup) for the long lm_head, where one row per wave made the launch
-  // VALU-bound (128256x2048: 46 us against 31 us without keys).
+  // Argmax keys are defined per 4 rows: no K split, and R rows per wave give R
+  // keys per workgroup. Very long matrices (the lm_head) take 4 rows per wave:
+  // they run many rounds of waves, each paying the load latency, so more bytes
+  // in flight per wave pay (128256x2048: 1 row per wave 46 us, 2 rows 33 us,
+  // 4 rows 27.5 us); at 8192 rows 4 per wave was 6% slower than 2.
   if (a.keys) {
-    if (a.K == 2048 && a.M % 2 == 0 && a.M >= 8192) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
+    if (a.K == 2048 && a.M % 4 == 0 && a.M >= 65536) launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
+    else if (a.K == 2048 && a.M % 2 == 0 && a.M >= 8192) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
     else if (a.K == 2048) launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
     else IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
     return check_launch("gemv_i4g32");
@@ -576,6 +579,10 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
   const bool r2 = a.M % 2 == 0 && a.M >= 8192;
   switch (a.K) {
     case 2048:
+      if (!PAIR && a.M % 4 == 0 && a.M >= 65536) {  // the lm_head shape: 31.3 -> 25.6 us
+        launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
+        break;
+      }
       if (r2) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
       else launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
       break;

@@ -227,6 +227,28 @@ def test_config4_swiglu_block(gpu, int4, mode):
         assert ops.max_abs_rel_l2(y, chain)[1] <= 2e-2
 
 
+@pytest.mark.parametrize("norm", [0, 2])
+def test_gemv_int4_long_matrix(gpu, norm):
+    """The lm_head-length int4 launch (4 rows per wave, >= 65536 rows), with a
+    partly inactive last workgroup (65540 rows), against the oracle."""
+    from iron_amd import _lib
+
+    M, K = 65540, 2048
+    g = torch.Generator().manual_seed(11)
+    W = (torch.randn(M, K, generator=g) * 0.02).to(BF16)
+    x = torch.randn(K, generator=g).to(BF16)
+    c, sc = _i4(W, gpu)
+    y = torch.empty(M, dtype=BF16, device=gpu)
+    _lib.call("iron_gemv_i4g32_fused", c.data_ptr(), sc.data_ptr(), None, None, x.to(gpu).data_ptr(), y.data_ptr(), M,
+              K, 1, norm, None, 1e-5, None, 0, None, _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    ref = ops.gemv_int4_reference(c.cpu(), sc.cpu(), x, out_dtype=torch.float32)
+    if norm == 2:  # NORM_SCALE: the product scaled by rsqrt(mean(x^2) + eps)
+        ref = ref * torch.rsqrt(x.float().pow(2).mean() + 1e-5)
+    mx, rl2 = ops.max_abs_rel_l2(y.cpu(), ref)
+    assert mx <= 2e-2 and rl2 <= 1e-2, (mx, rl2)
+
+
 @pytest.mark.parametrize("int4", [False, True])
 @pytest.mark.parametrize("M", [1000, 8194, 8196, 128256])
 def test_argmax_keys_and_select(gpu, int4, M):
