@@ -9,11 +9,11 @@
 // operands: C^T = B A^T).
 //
 // Tiles: a workgroup of WMW x WNW waves owns a (WMW*TI*32) x (WNW*TJ*32)
-// output tile; each wave owns TI x TJ MFMA tiles of 32x32. Four shapes are
+// output tile; each wave owns TI x TJ MFMA tiles of 32x32. Five shapes are
 // instantiated and gemm_launch picks one with a cost model: 256x256 (8 waves
-// of 64x128), 256x128 (8 waves of 64x64), 128x128 with 8 waves of 64x32 (one
-// workgroup per CU, 3 steps of look-ahead) and 128x128 with 4 waves of 64x64
-// (two workgroups per CU). Bigger tiles fetch fewer bytes per flop: at ~64
+// of 64x128), 256x192 (8 waves of 64x96, when it divides N), 256x128 (8 waves
+// of 64x64), 128x128 with 8 waves of 64x32 (one workgroup per CU, 3 steps of
+// look-ahead) and 128x128 with 4 waves of 64x64 (two workgroups per CU). Bigger tiles fetch fewer bytes per flop: at ~64
 // B/clk of L2->CU fill per CU, a 128x128x64 step needs as many cycles to fill
 // as its MFMAs take, a 256x256 step half as many. Two waves per SIMD hide each
 // other's LDS and barrier waits, which matters most when each CU has a single
@@ -90,6 +90,7 @@ using TileL = Tile<4, 2, 2, 4, 2>;   // 256x256, 8 waves of 64x128, 128 KiB
 using TileM = Tile<4, 2, 2, 2, 2>;   // 256x128, 8 waves of 64x64, 96 KiB
 using TileS = Tile<2, 4, 2, 1, 4>;   // 128x128, 8 waves of 64x32, 128 KiB, 3 steps ahead
 using TileS2 = Tile<2, 2, 2, 2, 2>;  // 128x128, 4 waves of 64x64, 64 KiB: two workgroups per CU
+using TileL3 = Tile<4, 2, 2, 3, 2>;  // 256x192, 8 waves of 64x96, 112 KiB: N = 3072 in 16 tiles
 
 // A 16-byte LDS access of 16 lanes covers all 64 banks once when their 16
 // consecutive rows use 16 distinct (row parity, slot) pairs: the slot is
@@ -549,7 +550,7 @@ static long long tile_count(const GemmArgs& a) {
 
 // Cost model: a launch takes ceil(tiles / slots) rounds, each costing a full
 // round of tile work at the shape's measured full-occupancy rate (TF/s on one
-// MI355X: 256x256 ~1000, 256x128 ~900, 128x128/4 waves ~800, 128x128/8 waves
+// MI355X: 256x256 ~1000, 256x192 ~900, 256x128 ~900, 128x128/4 waves ~800, 128x128/8 waves
 // ~660). Slots are workgroups resident at once: one per CU, two for the 64 KiB
 // shape. Fewer, bigger tiles win on large problems; a problem of one round of
 // 128x128 tiles gets the 8-wave shape.
@@ -572,8 +573,14 @@ static void launch_tile_i4(const GemmArgs& a, hipStream_t s) {
 static void gemm_launch(const GemmArgs& a, hipStream_t s) {
   const double cl = launch_cost<TileL>(a, 1, 1000.0), cm = launch_cost<TileM>(a, 1, 900.0);
   const double cs = launch_cost<TileS>(a, 1, 660.0), cs2 = launch_cost<TileS2>(a, 2, 800.0);
-  const double best = std::min(std::min(cl, cm), std::min(cs, cs2));
-  if (cs == best)
+  // 256x192 only where it divides N exactly (wave quantization: 3968x3072 gets 256 tiles instead of 192 of
+  // 256x256; 72 -> 57 us), and never for the SwiGLU pair epilogue, whose 64-column gate/up blocks must pair
+  // up inside a tile.
+  const double cl3 = (a.N % TileL3::BN == 0 && a.epi != kEpiSwigluPair) ? launch_cost<TileL3>(a, 1, 900.0) : 1e300;
+  const double best = std::min(std::min(std::min(cl, cm), std::min(cs, cs2)), cl3);
+  if (cl3 == best)
+    launch_tile<TileL3>(a, s);
+  else if (cs == best)
     launch_tile<TileS>(a, s);
   else if (cl == best)
     launch_tile<TileL>(a, s);

@@ -105,6 +105,8 @@ def test_prefill_gemm_shapes(gpu, M, K, N):
         (4000, 128, 4104),  # 256x256 tiles, ragged M and N
         (4096, 256, 4100),  # 256x256 tiles, odd row stride: element stores
         (3968, 2048, 2048),  # 256x128 tiles (prefill o_proj at 3968 tokens)
+        (3968, 256, 3072),  # 256x192 tiles (prefill qkv at 3968 tokens), ragged M
+        (3000, 64, 3072),  # 256x192 tiles, ragged M (184 rows in the last tile row)
         (2600, 64, 3300),  # 256x128 tiles, ragged, odd row stride
         (1280, 192, 4096),  # 128x128 tiles, more workgroups than CUs
         (1000, 192, 2050),  # 128x128 tiles, one workgroup per CU, ragged
