@@ -509,6 +509,62 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs a) {
   a.C[m * a.ldc + n] = f32_to_bf16(x);
 }
 
+// The same merge, 8 outputs per thread: 16-byte loads of every K range issued
+// up front (at most 8 ranges; clamped indexes, the extra ones dropped by
+// selects) and one 16-byte store. The sums run over the ranges in the same
+// order as above, so the results are identical. Needs N % 8 == 0, ldc % 8 == 0,
+// a 16-byte aligned C and M * N / 8 < 2^31 (checked on the host).
+__global__ __launch_bounds__(256) void gemm_splitk_reduce8_kernel(GemmArgs a) {
+  const int gpr = a.N >> 3;  // 8-output groups per row
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.M * gpr) return;
+  const int m = t / gpr, c = t - m * gpr;
+  const size_t mn4 = static_cast<size_t>(a.M) * a.N / 4;
+  const float4* p = reinterpret_cast<const float4*>(a.partial) + (static_cast<size_t>(m) * a.N >> 2) + 2 * c;
+  float4 u[8], v[8];
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+    const float4* q = p + static_cast<size_t>(min(kb, a.splits - 1)) * mn4;
+    u[kb] = q[0];
+    v[kb] = q[1];
+  }
+  float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < 8; ++kb) {
+    const bool live = kb < a.splits;
+    x[0] = live ? x[0] + u[kb].x : x[0];
+    x[1] = live ? x[1] + u[kb].y : x[1];
+    x[2] = live ? x[2] + u[kb].z : x[2];
+    x[3] = live ? x[3] + u[kb].w : x[3];
+    x[4] = live ? x[4] + v[kb].x : x[4];
+    x[5] = live ? x[5] + v[kb].y : x[5];
+    x[6] = live ? x[6] + v[kb].z : x[6];
+    x[7] = live ? x[7] + v[kb].w : x[7];
+  }
+  uint32_t h[4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (a.epi != EPI_NONE || a.clamp) {
+      x[e] = bf16_to_f32(f32_to_bf16(x[e]));
+      x[e] = apply_epilogue(x[e], a.epi);
+      if (a.clamp) x[e] = fminf(fmaxf(x[e], a.lo), a.hi);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    h[e] = static_cast<uint32_t>(f32_to_bf16(x[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(x[2 * e + 1])) << 16);
+  *reinterpret_cast<uint4*>(a.C + static_cast<size_t>(m) * a.ldc + 8 * c) = make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+static void launch_splitk_reduce(const GemmArgs& a, hipStream_t s) {
+  const long long mn = static_cast<long long>(a.M) * a.N;
+  if (a.splits <= 8 && a.N % 8 == 0 && a.ldc % 8 == 0 && aligned16(a.C) && aligned16(a.partial) &&
+      mn / 8 < (1LL << 31))
+    IRON_LAUNCH(gemm_splitk_reduce8_kernel, dim3(static_cast<unsigned>((mn / 8 + 255) / 256)), dim3(256), 0, s, a);
+  else
+    IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
+}
+
 // 64x64 tiled transpose through LDS: out (cols, rows) = in (rows, cols)^T.
 __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out,
                                                         int rows, int cols) {
@@ -638,8 +694,7 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, static_cast<float*>(workspace), splits};
   hipStream_t s = static_cast<hipStream_t>(stream);
   gemm_launch(a, s);
-  const long long mn = static_cast<long long>(M) * N;
-  IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
+  launch_splitk_reduce(a, s);
   return check_launch("gemm_bf16_nt_splitk");
 }
 
@@ -694,10 +749,7 @@ extern "C" int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* 
              static_cast<const uint16_t*>(scales), is_signed ? 1 : 0};
   hipStream_t s = static_cast<hipStream_t>(stream);
   gemm_i4_launch(a, s);
-  if (splits > 1) {
-    const long long mn = static_cast<long long>(M) * N;
-    IRON_LAUNCH(gemm_splitk_reduce_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, s, a);
-  }
+  if (splits > 1) launch_splitk_reduce(a, s);
   return check_launch("gemm_i4g32_nt");
 }
 

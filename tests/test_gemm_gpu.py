@@ -133,7 +133,8 @@ def test_gemm_tile_shapes(gpu, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N,splits", [(512, 8192, 2048, 4), (512, 2048, 2048, 4), (512, 2048, 3072, 2),
-                                          (100, 512, 200, 2), (256, 1024, 384, 8), (64, 4096, 64, 8)])
+                                          (100, 512, 200, 2), (100, 512, 203, 2), (256, 1024, 384, 8),
+                                          (64, 4096, 64, 8)])
 @pytest.mark.parametrize("epi,clamp", [(0, False), (2, False), (4, True)])
 def test_gemm_splitk(gpu, M, K, N, splits, epi, clamp):
     """Split-K GEMM (fp32 partials + ordered merge) against the fp32 reference
