@@ -24,7 +24,9 @@ launched one call at a time from Python.
 which is the timed region (HIP events on the launch stream around the K
 back-to-back launches) divided by K.
 ``cpu_baseline``: the CPU oracle (torch: dequantise, then fp32 matvec) timed
-on the host cores on a bounded sample. ``extra`` carries the other BASELINE
+on the host cores on a bounded sample; ``cpu_baseline.model_decode`` times the
+oracle's fp32 Llama forward (greedy decode, Llama-3.2-1B shape) the same way,
+beside the GPU decode rate in ``extra.model``. ``extra`` carries the other BASELINE
 configurations: bf16 GEMV (cfg 1), GQA decode (cfg 3), SwiGLU block bf16 and
 int4 (cfg 4), the prefill GEMM and the Llama-3.2-1B-shaped model (cfg 5:
 prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096 window).
@@ -429,6 +431,42 @@ def cpu_baseline_int4(torch, inputs, budget_s):
     }
 
 
+def cpu_baseline_model(torch, budget_s, prompt_len=16):
+    """The oracle's fp32 Llama forward (restated llama_cpu.py) on the host cores:
+    Llama-3.2-1B shape, random fp32 weights, a short prompt, then greedy decode
+    steps until the time budget is spent (a bounded sample of config 5's decode)."""
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, random_weights
+    from iron_amd.applications.llama_3_2_1b.model import compute_rope_angles
+    from oracle import llama as ollama
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = LlamaConfig()
+    t0 = time.perf_counter()
+    w = {k: v.float() for k, v in random_weights(cfg, torch.device("cpu"), seed=0).items()}
+    shape = ollama.LlamaShape(cfg.vocab_size, cfg.emb_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_groups, cfg.hidden_dim)
+    ref = ollama.LlamaCPU(shape, w, compute_rope_angles(cfg.head_dim, 1024, cfg.rope_base, cfg.rope_scaling))
+    setup_s = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g)
+    ref.reset()
+    logits = ref.forward(prompt)[0, -1]
+    steps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and prompt_len + steps < 1024:
+        logits = ref.forward(torch.tensor([[int(logits.argmax())]]))[0, -1]
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(steps / dt, 3),
+        "unit": "tok/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} greedy decode steps of the oracle's fp32 Llama forward (restated llama_cpu.py), "
+        f"Llama-3.2-1B shape, random weights, after a {prompt_len}-token prompt (KV {prompt_len}..{prompt_len + steps}); "
+        f"{dt:.1f} s (+{setup_s:.1f} s weight setup)",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -530,6 +568,7 @@ def main() -> int:
         out["extra"] = extra
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_int4(torch, i4["inputs"], args.cpu_seconds)
+            out["cpu_baseline"]["model_decode"] = cpu_baseline_model(torch, args.cpu_seconds)
     print(json.dumps(out), flush=True)
     return 0
 
