@@ -131,6 +131,17 @@ int iron_rmsnorm(const void* x, const void* residual, const void* w, void* out, 
 /* out = a + b, a * b over n bf16 (16-byte aligned). out may alias a or b.
  * Replace ElementwiseAdd / ElementwiseMul.get_callable() -> (a, b, out):
  * iron/operators/elementwise_add/op.py:12-24, elementwise_mul/op.py:12-24. */
+/* iron_rmsnorm with the residual operand given as the fp32 partial sums of a
+ * split-K GEMM (iron_gemm_nt_partials: `splits` ranges of rows*cols floats,
+ * 16-byte aligned; 1 <= splits <= 64): residual = bf16(sum of the ranges in
+ * order from 0), then s = bf16(x + residual), sum_out = s, out = norm(s) [* w]
+ * as iron_rmsnorm. Bit-identical to iron_gemm_bf16_nt_splitk + iron_rmsnorm.
+ * Fuses the GEMM merge into RMSNorm + ElementwiseAdd
+ * (iron/operators/rms_norm/op.py:19-122, elementwise_add/op.py:12-24) for
+ * the Llama prefill's o_proj and down_proj outputs (llama_npu.py:97-274). */
+int iron_rmsnorm_splitk(const void* x, const float* partial, int splits, const void* w, void* out, void* sum_out,
+                        int rows, int cols, float eps, void* stream);
+
 int iron_add(const void* a, const void* b, void* out, long long n, void* stream);
 int iron_mul(const void* a, const void* b, void* out, long long n, void* stream);
 
@@ -251,6 +262,21 @@ int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* scales, voi
                        long long ldc, int epilogue, int has_clamp, float clamp_lo, float clamp_hi, int is_signed,
                        int splits, void* workspace, long long workspace_bytes, void* stream);
 
+/* First pass of the split-K GEMMs alone, for a consumer that merges the
+ * partial sums itself (iron_rmsnorm_splitk, iron_qkv_rope_scatter_splitk):
+ * workspace (splits, M, N) fp32 receives A . B^T over each of `splits` equal
+ * K ranges (splits >= 1 divides K/64; splits*M*N*4 bytes, 16-byte aligned),
+ * with no merge, rounding or epilogue. B is bf16 (N, K) when codes is null,
+ * else the int4-g32 weights (codes, scales, is_signed) of iron_gemm_i4g32_nt;
+ * exactly one of B and codes is given. The consumers merge the ranges in order
+ * with the bf16 rounding of iron_gemm_bf16_nt_splitk, so every result is
+ * bit-identical to that GEMM followed by the consumer's plain form. Same
+ * reference operators as iron_gemm_bf16_nt / iron_gemm_i4g32_nt; it removes
+ * the merge pass (one launch and an M*N bf16 round trip) from the Llama
+ * prefill (llama_npu.py:97-274). */
+int iron_gemm_nt_partials(const void* A, const void* B, const void* codes, const void* scales, int is_signed,
+                          int M, int N, int K, int splits, void* workspace, long long workspace_bytes, void* stream);
+
 /* out (cols, rows) = in (rows, cols)^T, bf16. Layout glue for GEMM's
  * row-major B (the role of iron/operators/transpose/op.py:18-120). */
 int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream);
@@ -313,6 +339,16 @@ int iron_argmax_select(const void* keys, int n_keys, const void* table, int dim,
 int iron_qkv_rope_scatter(const void* qkv, const float* angles, int angle_rows, void* q_out, void* k_cache,
                           void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim, int max_len, int pos0,
                           void* stream);
+
+/* iron_qkv_rope_scatter with qkv given as the fp32 partial sums of a split-K
+ * GEMM (iron_gemm_nt_partials: `splits` ranges of seq*(H+2Hkv)*64 floats;
+ * 1 <= splits <= 64), each element merged as the GEMM's own merge (ranges in
+ * order from 0, one bf16 rounding) before the rotation. Bit-identical to
+ * iron_gemm_bf16_nt_splitk + iron_qkv_rope_scatter. Same reference steps as
+ * iron_qkv_rope_scatter, with the GEMM merge folded in. */
+int iron_qkv_rope_scatter_splitk(const float* partial, int splits, const float* angles, int angle_rows, void* q_out,
+                                 void* k_cache, void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim,
+                                 int max_len, int pos0, void* stream);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,9 @@ SIGNATURES: dict[str, list] = {
     "iron_argmax_bf16": [_P, _I, _P, _P, _P, _I, _P],
     "iron_argmax_select": [_P, _I, _P, _I, _I, _P, _P, _P, _P, _I, _P],
     "iron_qkv_rope_scatter": [_P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "iron_qkv_rope_scatter_splitk": [_P, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
+    "iron_rmsnorm_splitk": [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P],
+    "iron_gemm_nt_partials": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _LL, _P],
 }
 
 # ... except these queries, which return a value.

@@ -64,6 +64,10 @@ class LlamaConfig:
     # prefill GEMMs dequantise the int4 weights in the kernel instead of
     # keeping bf16 copies (bit-identical results, ~1.7 GB less memory)
     prefill_int4: bool = False
+    # split-K prefill GEMMs leave their fp32 partial sums to the next kernel
+    # (RoPE scatter, RMSNorm), which merges them: one launch fewer per split
+    # GEMM, bit-identical results
+    prefill_fuse_merge: bool = True
 
     @property
     def head_dim(self) -> int:
@@ -204,6 +208,23 @@ class Linear:
         else:
             _lib.call("iron_gemm_bf16_nt", X.data_ptr(), self._bf16.data_ptr(), Y.data_ptr(), rows, self.N, self.K,
                       self.N, 0, 0, 0.0, 0.0, stream)
+
+
+    def gemm_partials(self, X, rows, stream, workspace):
+        """The first pass of the split-K GEMM alone: fp32 partial sums of X . W^T,
+        (splits, rows, N) in ``workspace(nbytes)``, for a consumer that merges
+        them (iron_rmsnorm_splitk, iron_qkv_rope_scatter_splitk). Returns
+        (partials, splits), or None when this shape is not split (use gemm)."""
+        splits = _lib.query("iron_gemm_splitk_choose", rows, self.N, self.K)
+        if splits < 2:
+            return None
+        need = int(_lib.query("iron_gemm_splitk_workspace_bytes", rows, self.N, splits))
+        ws = workspace(need)
+        i4 = self._bf16 is None
+        _lib.call("iron_gemm_nt_partials", X.data_ptr(), _lib.ptr(None if i4 else self._bf16),
+                  _lib.ptr(self.codes if i4 else None), _lib.ptr(self.scales if i4 else None), 1, rows, self.N,
+                  self.K, splits, ws.data_ptr(), need, stream)
+        return ws, splits
 
 
 class LlamaHIP:
@@ -415,25 +436,41 @@ class LlamaHIP:
         X, Xn, T = b["X"], b["Xn"], b["T"]
         _lib.call("iron_embedding", self.embed.data_ptr(), b["ids"].data_ptr(), X.data_ptr(), S, E, cfg.vocab_size, s)
         scale = 1.0 / math.sqrt(Hd)
-        first = True
+        eps = float(cfg.eps)
+
+        def linear(L, Xin, Yout):
+            """Yout = Xin . W^T, or None with the split-K partials returned for the next kernel to merge."""
+            part = L.gemm_partials(Xin, S, s, self._workspace) if cfg.prefill_fuse_merge else None
+            if part is None:
+                L.gemm(Xin, Yout, S, s, self._workspace)
+            return part
+
+        def add_norm(part):
+            """X += T (or the merged partials of the GEMM that produced it); Xn = norm(X)."""
+            if part is None:
+                _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E, eps, s)
+            else:
+                _lib.call("iron_rmsnorm_splitk", X.data_ptr(), part[0].data_ptr(), part[1], None, Xn.data_ptr(),
+                          X.data_ptr(), S, E, eps, s)
+
+        pending = None  # partials of the previous layer's down projection
         for i, L in enumerate(self.layers):
             # norm weights are folded into the next matrices: unweighted RMSNorm
-            if first:
-                _lib.call("iron_rmsnorm", X.data_ptr(), None, None, Xn.data_ptr(), None, S, E, float(cfg.eps), s)
-                first = False
-            else:  # X += T (previous FFN output), Xn = norm(X)
-                _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
-                          float(cfg.eps), s)
-            L["qkv"].gemm(Xn, b["QKV"], S, s, self._workspace)
-            _lib.call("iron_qkv_rope_scatter", b["QKV"].data_ptr(), self.angles.data_ptr(), self.angles.shape[0],
-                      b["Q"].data_ptr(), self.k_cache[i].data_ptr(), self.v_cache[i].data_ptr(), S, cfg.n_heads,
-                      cfg.n_kv_groups, Hd, cfg.max_seq_len, pos0, s)
+            if i == 0:
+                _lib.call("iron_rmsnorm", X.data_ptr(), None, None, Xn.data_ptr(), None, S, E, eps, s)
+            else:  # X += previous FFN output, Xn = norm(X)
+                add_norm(pending)
+            part = linear(L["qkv"], Xn, b["QKV"])
+            rope_args = (self.angles.data_ptr(), self.angles.shape[0], b["Q"].data_ptr(), self.k_cache[i].data_ptr(),
+                         self.v_cache[i].data_ptr(), S, cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, pos0, s)
+            if part is None:
+                _lib.call("iron_qkv_rope_scatter", b["QKV"].data_ptr(), *rope_args)
+            else:
+                _lib.call("iron_qkv_rope_scatter_splitk", part[0].data_ptr(), part[1], *rope_args)
             _lib.call("iron_attention_prefill", b["Q"].data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), b["O"].data_ptr(), cfg.n_heads, cfg.n_kv_groups, S, pos0 + S, Hd,
                       Hd, cfg.n_heads * Hd, cfg.max_seq_len * Hd, Hd, Hd, cfg.n_heads * Hd, S, 1, pos0, scale, s)
-            L["o"].gemm(b["O"], T, S, s, self._workspace)
-            _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
-                      float(cfg.eps), s)
+            add_norm(linear(L["o"], b["O"], T))
             if "gate_up" in L:  # G = silu(Xn Wg^T) * (Xn Wu^T) in one GEMM
                 _lib.call("iron_gemm_bf16_nt_swiglu", Xn.data_ptr(), L["gate_up"].data_ptr(), b["G"].data_ptr(), S,
                           cfg.hidden_dim, E, cfg.hidden_dim, s)
@@ -442,9 +479,8 @@ class LlamaHIP:
                 L["up"].gemm(Xn, b["U"], S, s, self._workspace)
                 _lib.call("iron_silu_mul", b["G"].data_ptr(), b["U"].data_ptr(), b["G"].data_ptr(),
                           S * cfg.hidden_dim, s)
-            L["down"].gemm(b["G"], T, S, s, self._workspace)
-        _lib.call("iron_rmsnorm", X.data_ptr(), T.data_ptr(), None, Xn.data_ptr(), X.data_ptr(), S, E,
-                  float(cfg.eps), s)
+            pending = linear(L["down"], b["G"], T)
+        add_norm(pending)
         self.head.gemv(Xn[S - 1], self.logits, s, keys=self.keys)
         self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
         self.host_pos = pos0 + S

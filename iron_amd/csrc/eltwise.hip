@@ -29,11 +29,15 @@ __device__ __forceinline__ float block_reduce(float v, float* smem) {
 
 // ------------------------------------------------------------------ RMSNorm
 // s = x (+ residual); sum_out = s (when requested); out = s * rsqrt(mean(s^2)+eps) [* w]
-template <int CPT>
+// PART: the residual is a split-K GEMM output given as its fp32 partial sums
+// (splits ranges of rows*cols floats each), merged here as the GEMM's own merge
+// does (range order from 0, one bf16 rounding) before the add.
+template <int CPT, bool PART = false>
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                          const uint16_t* __restrict__ resid,
                                                          const uint16_t* __restrict__ w, uint16_t* out,
-                                                         uint16_t* sum_out, int cols, float eps) {
+                                                         uint16_t* sum_out, int cols, float eps,
+                                                         const float* __restrict__ part, int splits) {
   __shared__ float smem[kBlock / kWave];
   const size_t row = blockIdx.x;
   const int nch = cols >> 3;
@@ -52,7 +56,19 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(const uint16_t* __restr
         v[i][2 * e] = lo_bf16(wa[e]);
         v[i][2 * e + 1] = hi_bf16(wa[e]);
       }
-      if (rr) {
+      if (PART) {
+        const size_t range4 = static_cast<size_t>(gridDim.x) * cols / 4;  // float4s per K range
+        const float4* pp = reinterpret_cast<const float4*>(part + row * cols) + 2 * c;
+        float r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb < splits; ++kb) {
+          const float4 u = pp[kb * range4], q = pp[kb * range4 + 1];
+          r[0] += u.x; r[1] += u.y; r[2] += u.z; r[3] += u.w;
+          r[4] += q.x; r[5] += q.y; r[6] += q.z; r[7] += q.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          v[i][e] = bf16_to_f32(f32_to_bf16(v[i][e] + bf16_to_f32(f32_to_bf16(r[e]))));
+      } else if (rr) {
         const uint4 b = rr[c];
         const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
@@ -277,11 +293,36 @@ extern "C" int iron_rmsnorm(const void* x, const void* residual, const void* w, 
   auto O = static_cast<uint16_t*>(out);
   auto S = static_cast<uint16_t*>(sum_out);
   dim3 g(rows), b(kBlock);
-  if (cpt <= 1) IRON_LAUNCH((rmsnorm_kernel<1>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else if (cpt <= 2) IRON_LAUNCH((rmsnorm_kernel<2>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else if (cpt <= 4) IRON_LAUNCH((rmsnorm_kernel<4>), g, b, 0, s, X, R, W, O, S, cols, eps);
-  else IRON_LAUNCH((rmsnorm_kernel<8>), g, b, 0, s, X, R, W, O, S, cols, eps);
+  if (cpt <= 1) IRON_LAUNCH((rmsnorm_kernel<1>), g, b, 0, s, X, R, W, O, S, cols, eps, nullptr, 0);
+  else if (cpt <= 2) IRON_LAUNCH((rmsnorm_kernel<2>), g, b, 0, s, X, R, W, O, S, cols, eps, nullptr, 0);
+  else if (cpt <= 4) IRON_LAUNCH((rmsnorm_kernel<4>), g, b, 0, s, X, R, W, O, S, cols, eps, nullptr, 0);
+  else IRON_LAUNCH((rmsnorm_kernel<8>), g, b, 0, s, X, R, W, O, S, cols, eps, nullptr, 0);
   return check_launch("rmsnorm");
+}
+
+extern "C" int iron_rmsnorm_splitk(const void* x, const float* partial, int splits, const void* w, void* out,
+                                   void* sum_out, int rows, int cols, float eps, void* stream) {
+  IRON_REQUIRE(x && partial && out, "iron_rmsnorm_splitk: null pointer");
+  IRON_REQUIRE(splits >= 1 && splits <= 64, "iron_rmsnorm_splitk: splits=%d outside [1, 64]", splits);
+  IRON_REQUIRE(rows > 0 && cols > 0 && cols % 8 == 0,
+               "iron_rmsnorm_splitk: rows=%d cols=%d (cols must be a multiple of 8)", rows, cols);
+  IRON_REQUIRE(cols <= kBlock * kMaxChunksPerThread * 8, "iron_rmsnorm_splitk: cols=%d exceeds %d", cols,
+               kBlock * kMaxChunksPerThread * 8);
+  IRON_REQUIRE(aligned16(x) && aligned16(out) && aligned16(partial) && (!w || aligned16(w)) &&
+                   (!sum_out || aligned16(sum_out)),
+               "iron_rmsnorm_splitk: operands must be 16-byte aligned");
+  const int cpt = (cols / 8 + kBlock - 1) / kBlock;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto X = static_cast<const uint16_t*>(x);
+  auto W = static_cast<const uint16_t*>(w);
+  auto O = static_cast<uint16_t*>(out);
+  auto S = static_cast<uint16_t*>(sum_out);
+  dim3 g(rows), b(kBlock);
+  if (cpt <= 1) IRON_LAUNCH((rmsnorm_kernel<1, true>), g, b, 0, s, X, nullptr, W, O, S, cols, eps, partial, splits);
+  else if (cpt <= 2) IRON_LAUNCH((rmsnorm_kernel<2, true>), g, b, 0, s, X, nullptr, W, O, S, cols, eps, partial, splits);
+  else if (cpt <= 4) IRON_LAUNCH((rmsnorm_kernel<4, true>), g, b, 0, s, X, nullptr, W, O, S, cols, eps, partial, splits);
+  else IRON_LAUNCH((rmsnorm_kernel<8, true>), g, b, 0, s, X, nullptr, W, O, S, cols, eps, partial, splits);
+  return check_launch("rmsnorm_splitk");
 }
 
 extern "C" int iron_add(const void* a, const void* b, void* out, long long n, void* stream) {

@@ -753,6 +753,36 @@ extern "C" int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* 
   return check_launch("gemm_i4g32_nt");
 }
 
+extern "C" int iron_gemm_nt_partials(const void* A, const void* B, const void* codes, const void* scales,
+                                     int is_signed, int M, int N, int K, int splits, void* workspace,
+                                     long long workspace_bytes, void* stream) {
+  const bool i4 = codes != nullptr;
+  IRON_REQUIRE(i4 != (B != nullptr), "iron_gemm_nt_partials: give exactly one of B (bf16) and codes (int4-g32)");
+  if (int rc = gemm_check("iron_gemm_nt_partials", A, i4 ? codes : B, workspace, M, N, K, N, EPI_NONE, 0, 0.f, 0.f))
+    return rc;
+  IRON_REQUIRE(!i4 || (scales && (reinterpret_cast<uintptr_t>(scales) & 3u) == 0),
+               "iron_gemm_nt_partials: scales must be non-null and 4-byte aligned");
+  IRON_REQUIRE(splits >= 1 && (K / BK) % splits == 0,
+               "iron_gemm_nt_partials: splits=%d must divide the %d K steps of 64", splits, K / BK);
+  const long long tiles =
+      static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile) * splits;
+  const long long need = static_cast<long long>(splits) * M * N * 4;
+  IRON_REQUIRE(tiles < (1LL << 31) && static_cast<long long>(M) * N < (1LL << 38),
+               "iron_gemm_nt_partials: problem too large");
+  IRON_REQUIRE(workspace_bytes >= need, "iron_gemm_nt_partials: workspace of %lld bytes < %lld", workspace_bytes,
+               need);
+  IRON_REQUIRE(aligned16(workspace), "iron_gemm_nt_partials: workspace must be 16-byte aligned");
+  GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), nullptr, M, N, K, N, EPI_NONE, 0,
+             0.f, 0.f, static_cast<float*>(workspace), splits, static_cast<const uint8_t*>(codes),
+             static_cast<const uint16_t*>(scales), is_signed ? 1 : 0};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (i4)
+    gemm_i4_launch(a, s);
+  else
+    gemm_launch(a, s);
+  return check_launch("gemm_nt_partials");
+}
+
 extern "C" int iron_transpose_bf16(const void* in, void* out, int rows, int cols, void* stream) {
   IRON_REQUIRE(in && out && in != out, "iron_transpose_bf16: null or aliased pointers");
   IRON_REQUIRE(rows > 0 && cols > 0, "iron_transpose_bf16: empty matrix");

@@ -32,6 +32,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(cvt_pk_bf16(f, 0.f) & 0xffffu);
 }
 
+// One output element of a split-K GEMM from its fp32 partial sums (range kb at
+// p[kb * stride]): summed in range order starting from 0 and rounded once to
+// bf16, which is the split-K merge of the GEMMs with no epilogue.
+__device__ __forceinline__ float merged_bf16(const float* p, size_t stride, int splits) {
+  float x = 0.f;
+  for (int kb = 0; kb < splits; ++kb) x += p[kb * stride];
+  return bf16_to_f32(f32_to_bf16(x));
+}
+
 // Low / high bf16 of a packed 32-bit word, widened to fp32.
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -123,11 +123,15 @@ __global__ __launch_bounds__(1024) void select_embed_kernel(const unsigned long 
 
 // Prefill: qkv (S, (H + 2*Hkv) * 64) rows -> q_out (S, H*64) rotated,
 // k_cache[:, pos0+s] rotated, v_cache[:, pos0+s] copied. One thread per
-// rotated pair (q and k heads) or per v element pair.
+// rotated pair (q and k heads) or per v element pair. PART: qkv is a split-K
+// GEMM output given as its fp32 partial sums (splits ranges of S*(H+2Hkv)*64
+// floats), merged here exactly as the GEMM's own merge.
+template <bool PART>
 __global__ __launch_bounds__(256) void qkv_scatter_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ angles,
                                                           uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
                                                           uint16_t* __restrict__ v_cache, int S, int H, int Hkv,
-                                                          int max_len, int pos0) {
+                                                          int max_len, int pos0, const float* __restrict__ part,
+                                                          int splits) {
   constexpr int D = 64;
   const int heads = H + 2 * Hkv;
   const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
@@ -136,10 +140,13 @@ __global__ __launch_bounds__(256) void qkv_scatter_kernel(const uint16_t* __rest
   const int rem = static_cast<int>(t % (heads * 32));
   const int h = rem / 32, i = rem % 32;
   const int p = pos0 + s;
-  const uint16_t* row = qkv + static_cast<size_t>(s) * heads * D + h * D;
+  const size_t off = static_cast<size_t>(s) * heads * D + h * D;
+  const uint16_t* row = PART ? nullptr : qkv + off;
+  const size_t range = static_cast<size_t>(S) * heads * D;
+  auto val = [&](int col) { return PART ? merged_bf16(part + off + col, range, splits) : bf16_to_f32(row[col]); };
   if (h < H + Hkv) {
     const float c = angles[static_cast<size_t>(p) * D + 2 * i], sn = angles[static_cast<size_t>(p) * D + 2 * i + 1];
-    const float x1 = bf16_to_f32(row[i]), x2 = bf16_to_f32(row[i + 32]);
+    const float x1 = val(i), x2 = val(i + 32);
     const uint16_t y1 = f32_to_bf16(x1 * c - x2 * sn), y2 = f32_to_bf16(x2 * c + x1 * sn);
     uint16_t* dst = h < H ? q_out + static_cast<size_t>(s) * H * D + h * D
                           : k_cache + (static_cast<size_t>(h - H) * max_len + p) * D;
@@ -147,8 +154,8 @@ __global__ __launch_bounds__(256) void qkv_scatter_kernel(const uint16_t* __rest
     dst[i + 32] = y2;
   } else {
     uint16_t* dst = v_cache + (static_cast<size_t>(h - H - Hkv) * max_len + p) * D;
-    dst[i] = row[i];
-    dst[i + 32] = row[i + 32];
+    dst[i] = PART ? f32_to_bf16(val(i)) : row[i];
+    dst[i + 32] = PART ? f32_to_bf16(val(i + 32)) : row[i + 32];
   }
 }
 
@@ -201,9 +208,27 @@ extern "C" int iron_qkv_rope_scatter(const void* qkv, const float* angles, int a
                "iron_qkv_rope_scatter: positions [%d, %d) exceed the cache (%d) or angle table (%d)", pos0,
                pos0 + seq, max_len, angle_rows);
   const long long threads = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
-  IRON_LAUNCH(qkv_scatter_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+  IRON_LAUNCH(qkv_scatter_kernel<false>, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), angles,
                      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
-                     seq, n_heads, n_kv_heads, max_len, pos0);
+                     seq, n_heads, n_kv_heads, max_len, pos0, nullptr, 0);
   return check_launch("qkv_rope_scatter");
+}
+
+extern "C" int iron_qkv_rope_scatter_splitk(const float* partial, int splits, const float* angles, int angle_rows,
+                                            void* q_out, void* k_cache, void* v_cache, int seq, int n_heads,
+                                            int n_kv_heads, int head_dim, int max_len, int pos0, void* stream) {
+  IRON_REQUIRE(partial && angles && q_out && k_cache && v_cache, "iron_qkv_rope_scatter_splitk: null pointer");
+  IRON_REQUIRE(splits >= 1 && splits <= 64, "iron_qkv_rope_scatter_splitk: splits=%d outside [1, 64]", splits);
+  IRON_REQUIRE(head_dim == 64, "iron_qkv_rope_scatter_splitk: head_dim=%d (only 64 is supported)", head_dim);
+  IRON_REQUIRE(seq > 0 && n_heads > 0 && n_kv_heads > 0, "iron_qkv_rope_scatter_splitk: empty shape");
+  IRON_REQUIRE(pos0 >= 0 && pos0 + seq <= max_len && pos0 + seq <= angle_rows,
+               "iron_qkv_rope_scatter_splitk: positions [%d, %d) exceed the cache (%d) or angle table (%d)", pos0,
+               pos0 + seq, max_len, angle_rows);
+  const long long threads = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
+  IRON_LAUNCH(qkv_scatter_kernel<true>, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+              static_cast<hipStream_t>(stream), nullptr, angles, static_cast<uint16_t*>(q_out),
+              static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq, n_heads, n_kv_heads, max_len, pos0,
+              partial, splits);
+  return check_launch("qkv_rope_scatter_splitk");
 }

@@ -49,3 +49,23 @@ def test_abi_version_and_error_path():
         _lib.call("iron_gemv_bf16", None, None, None, 16, 16, 1, 0, None)
     with pytest.raises(_lib.IronHipError, match="multiple of 8"):
         _lib.call("iron_gemv_bf16", 16, 16, 16, 16, 12, 1, 0, None)
+
+
+def test_splitk_consumer_argument_errors():
+    """The split-K partials entry point and its consumers reject bad arguments
+    on the host, before any launch."""
+    from iron_amd import _lib
+
+    with pytest.raises(_lib.IronHipError, match="exactly one of B"):
+        _lib.call("iron_gemm_nt_partials", 16, 16, 16, 16, 1, 64, 64, 128, 2, 16, 1 << 20, None)
+    with pytest.raises(_lib.IronHipError, match="must divide"):
+        _lib.call("iron_gemm_nt_partials", 16, 16, None, None, 1, 64, 64, 192, 2, 16, 1 << 20, None)
+    with pytest.raises(_lib.IronHipError, match="workspace of"):
+        _lib.call("iron_gemm_nt_partials", 16, 16, None, None, 1, 64, 64, 128, 2, 16, 100, None)
+    with pytest.raises(_lib.IronHipError, match="splits=0"):
+        _lib.call("iron_rmsnorm_splitk", 16, 16, 0, None, 16, 16, 4, 64, 1e-5, None)
+    with pytest.raises(_lib.IronHipError, match="multiple of 8"):
+        _lib.call("iron_rmsnorm_splitk", 16, 16, 2, None, 16, 16, 4, 60, 1e-5, None)
+    with pytest.raises(_lib.IronHipError, match="exceed the cache"):
+        _lib.call("iron_qkv_rope_scatter_splitk", 16, 2, 16, 64, 16, 16, 16, 8, 4, 2, 64, 64, 60, None)
+

@@ -136,3 +136,36 @@ def test_prefill_from_int4_bitwise(gpu):
         outs.append((toks, model.logits.clone().view(torch.int16)))
     assert outs[0][0] == outs[1][0]
     assert torch.equal(outs[0][1], outs[1][1])
+
+
+MID = dict(vocab_size=1000, emb_dim=1024, n_layers=2, n_heads=16, n_kv_groups=4, hidden_dim=2048, max_seq_len=320)
+
+
+@pytest.mark.parametrize("prefill_int4", [False, True])
+def test_prefill_fused_merge_bit_identical(gpu, prefill_int4):
+    """LlamaConfig(prefill_fuse_merge=True): the split-K GEMMs' partial sums are
+    merged by the RoPE scatter and the RMSNorm that consume them. Logits and KV
+    caches must equal, bit for bit, those of the GEMMs' own merge, for a prompt
+    and for a continuation at a later position."""
+    import dataclasses
+
+    from iron_amd import _lib
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
+
+    cfg = LlamaConfig(prefill_int4=prefill_int4, **MID)
+    # at these shapes qkv and o_proj split K in 2 ranges, down_proj in 4
+    assert _lib.query("iron_gemm_splitk_choose", 64, 1536, 1024) == 2
+    assert _lib.query("iron_gemm_splitk_choose", 64, 1024, 2048) == 4
+    w = random_weights(cfg, gpu, seed=4)
+    fused = LlamaHIP(cfg, w, device=gpu)
+    plain = LlamaHIP(dataclasses.replace(cfg, prefill_fuse_merge=False), w, device=gpu)
+    for m in (fused, plain):
+        m.reset()
+    for chunk in (list(range(3, 67)), [5, 900, 17, 4, 4, 250, 61]):
+        for m in (fused, plain):
+            m.prefill(chunk)
+        torch.cuda.synchronize()
+        assert torch.equal(fused.logits, plain.logits)
+        for i in range(cfg.n_layers):
+            assert torch.equal(fused.k_cache[i], plain.k_cache[i])
+            assert torch.equal(fused.v_cache[i], plain.v_cache[i])
