@@ -26,7 +26,7 @@ back-to-back launches) divided by K.
 ``cpu_baseline``: the CPU oracle (torch: dequantise, then fp32 matvec) timed
 on the host cores on a bounded sample; ``cpu_baseline.model_decode`` times the
 oracle's fp32 Llama forward (greedy decode, Llama-3.2-1B shape) the same way,
-beside the GPU decode rate in ``extra.model``. ``extra`` carries the other BASELINE
+beside the GPU decode rate in ``extra.llama_cfg5``. ``extra`` carries the other BASELINE
 configurations: bf16 GEMV (cfg 1), GQA decode (cfg 3), SwiGLU block bf16 and
 int4 (cfg 4), the prefill GEMM and the Llama-3.2-1B-shaped model (cfg 5:
 prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096 window).
@@ -54,7 +54,7 @@ METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE +
 # WRITE_SIZE, each scaled by the counter's reading for a copy of known size
 # (profiles/gemv_i4g32_cfg2_pmc.md).
-TRAFFIC_BYTES = 9541893
+TRAFFIC_BYTES = 9551129
 
 
 class Timer:
