@@ -69,3 +69,11 @@ def test_splitk_consumer_argument_errors():
     with pytest.raises(_lib.IronHipError, match="exceed the cache"):
         _lib.call("iron_qkv_rope_scatter_splitk", 16, 2, 16, 64, 16, 16, 16, 8, 4, 2, 64, 64, 60, None)
 
+
+
+def test_time_next_launch_argument_error():
+    from iron_amd import _lib
+
+    with pytest.raises(_lib.IronHipError, match="both events or neither"):
+        _lib.call("iron_time_next_launch", 16, None)
+    _lib.call("iron_time_next_launch", None, None)  # disarm: always accepted

@@ -332,3 +332,46 @@ def test_gemv_int4_fused_modes(gpu, M, K, mode, pair):
     assert rel_l2 <= 1e-2, rel_l2
     bad = ops.within_bf16_ulps(y, ref, n_ulp=2.0, atol=2e-2)
     assert not bad, (max_abs, [(i, float(y[i]), float(ref[i])) for i in bad[:5]])
+
+
+def test_time_next_launch(gpu):
+    """iron_time_next_launch arms two events for the next entry-point call only:
+    its kernels record them (start of the first, end of the last), a call that
+    fails validation disarms them, and results do not change."""
+    from iron_amd import _lib
+
+    s = _lib.stream_handle(gpu)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    b.record()
+    torch.cuda.synchronize()  # both events exist and have completed
+    t0 = a.elapsed_time(b)
+    M, K = 4096, 2048
+    g = torch.Generator().manual_seed(3)
+    W = (torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu)
+    x = torch.randn(K, generator=g).to(torch.bfloat16).to(gpu)
+    y0 = torch.empty(M, dtype=torch.bfloat16, device=gpu)
+    y1 = torch.empty(M, dtype=torch.bfloat16, device=gpu)
+    _lib.call("iron_gemv_bf16", W.data_ptr(), x.data_ptr(), y0.data_ptr(), M, K, 1, 0, s)
+    # armed, then a call that fails validation: disarmed, so the next call records nothing
+    _lib.call("iron_time_next_launch", a.cuda_event, b.cuda_event)
+    with pytest.raises(_lib.IronHipError, match="multiple of 8"):
+        _lib.call("iron_gemv_bf16", W.data_ptr(), x.data_ptr(), y1.data_ptr(), M, 12, 1, 0, s)
+    _lib.call("iron_gemv_bf16", W.data_ptr(), x.data_ptr(), y1.data_ptr(), M, K, 1, 0, s)
+    torch.cuda.synchronize()
+    assert a.elapsed_time(b) == t0
+    # armed for a two-kernel call (split-K GEMM: partial pass + merge) and then one GEMV
+    A = (torch.randn(64, K, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    C = torch.empty(64, M, dtype=torch.bfloat16, device=gpu)
+    need = int(_lib.query("iron_gemm_splitk_workspace_bytes", 64, M, 4))
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    _lib.call("iron_time_next_launch", a.cuda_event, b.cuda_event)
+    _lib.call("iron_gemm_bf16_nt_splitk", A.data_ptr(), W.data_ptr(), C.data_ptr(), 64, M, K, M, 0, 0, 0.0, 0.0, 4,
+              ws.data_ptr(), need, s)
+    _lib.call("iron_gemv_bf16", W.data_ptr(), x.data_ptr(), y1.data_ptr(), M, K, 1, 0, s)
+    torch.cuda.synchronize()
+    t_gemm = a.elapsed_time(b)
+    assert 0.0 < t_gemm < 50.0, t_gemm
+    assert torch.equal(y0, y1)
+    with pytest.raises(_lib.IronHipError, match="both events"):
+        _lib.call("iron_time_next_launch", a.cuda_event, None)
