@@ -11,6 +11,7 @@ _OPERATOR_MODULES = {
     "Dequant": "dequant",
     "ElementwiseAdd": "elementwise_add",
     "ElementwiseMul": "elementwise_mul",
+    "GELU": "gelu",
     "GEMM": "gemm",
     "GEMMInt4": "gemm_int4",
     "GEMV": "gemv",

@@ -166,3 +166,46 @@ def test_rope_fp32_table_llama_decode_shape(gpu):
     ref = ops.rope_reference(x, row)
     bad = ops.within_bf16_ulps(out, ops.rope_reference(x, row).float(), n_ulp=1.0)
     assert not bad and torch.allclose(out.cpu().float(), ref.float(), atol=2e-2)
+
+
+@pytest.mark.parametrize("size,cols,chans,tile", [(2048, 1, 1, 2048), (8192, 8, 2, 1024), (65536, 4, 1, 4096)])
+def test_gelu(gpu, size, cols, chans, tile):
+    """GELU (tanh form) against the oracle at the reference test's tolerance
+    (iron/operators/gelu/test.py:47: relative 0.04, absolute 1e-6), on inputs in
+    [-4, 4] (both tails of the tanh)."""
+    from iron_amd.operators import GELU
+
+    g = torch.Generator().manual_seed(size + cols)
+    x = (torch.rand(size, generator=g) * 8 - 4).to(BF16)
+    out = torch.empty(size, dtype=BF16, device=gpu)
+    GELU(size=size, num_aie_columns=cols, num_channels=chans, tile_size=tile).get_callable()(x.to(gpu), out)
+    torch.cuda.synchronize()
+    ref = ops.gelu_tanh(x).to(BF16)
+    assert not ops.verify_buffer(out, ref, rel_tol=0.04, abs_tol=1e-6)
+
+
+@pytest.mark.parametrize("n", [1, 1025, 128256])
+def test_argmax_bf16(gpu, n):
+    """Greedy argmax over bf16 logits: the first index of the maximum (ties
+    planted), the history write at *pos when pos < history_cap, and pos += 1."""
+    from iron_amd import _lib
+
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=g).to(BF16)
+    if n > 1000:
+        x[n // 3] = x[n - 1] = 9.0  # tie: the first index wins
+    s = _lib.stream_handle(gpu)
+    xd = x.to(gpu)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=gpu)
+    pos = torch.tensor([3], dtype=torch.int32, device=gpu)
+    hist = torch.full((8,), -1, dtype=torch.int32, device=gpu)
+    _lib.call("iron_argmax_bf16", xd.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), hist.data_ptr(), 8, s)
+    torch.cuda.synchronize()
+    want = int(torch.argmax(x.float()))
+    assert int(tok) == want and (n <= 1000 or want == n // 3)
+    assert int(pos) == 4 and int(hist[3]) == want and int((hist != -1).sum()) == 1
+    pos.fill_(8)  # at the history capacity: no write, position still advances
+    _lib.call("iron_argmax_bf16", xd.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), hist.data_ptr(), 8, s)
+    _lib.call("iron_argmax_bf16", xd.data_ptr(), n, tok.data_ptr(), None, None, 0, s)  # token only
+    torch.cuda.synchronize()
+    assert int(pos) == 9 and int((hist != -1).sum()) == 1 and int(tok) == want
