@@ -77,3 +77,20 @@ def test_time_next_launch_argument_error():
     with pytest.raises(_lib.IronHipError, match="both events or neither"):
         _lib.call("iron_time_next_launch", 16, None)
     _lib.call("iron_time_next_launch", None, None)  # disarm: always accepted
+
+
+def test_operator_catalog_resolves():
+    """Every name of the lazy operator catalog (iron/operators/__init__.py:13-47
+    counterpart) imports and is an operator class with the reference's
+    get_arg_spec / get_callable surface; unknown names raise AttributeError."""
+    import iron_amd.operators as catalog
+
+    for name in catalog.__all__:
+        obj = getattr(catalog, name)
+        if name == "flm":
+            assert hasattr(obj, "GEMM")
+            continue
+        assert isinstance(obj, type) and obj.__name__ == name, name
+        assert hasattr(obj, "get_arg_spec") and hasattr(obj, "get_callable"), name
+    with pytest.raises(AttributeError):
+        getattr(catalog, "NoSuchOperator")
