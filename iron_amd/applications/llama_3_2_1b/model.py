@@ -292,6 +292,7 @@ class LlamaHIP:
         self.host_pos = 0
         self.graph = None
         self._prefill_bufs = {}
+        self._prefill_graphs = {}  # (prompt length, start position) -> captured prefill
         self._gemm_ws = torch.empty(0, dtype=torch.uint8, device=dev)
         torch.cuda.synchronize(dev)
 
@@ -397,8 +398,10 @@ class LlamaHIP:
 
     # ------------------------------------------------------------ prefill
     def _workspace(self, nbytes: int) -> torch.Tensor:
-        """Split-K GEMM workspace of at least ``nbytes`` (grown on demand; stream-ordered reuse)."""
+        """Split-K GEMM workspace of at least ``nbytes`` (grown on demand; stream-ordered reuse).
+        Growing it drops the captured prefill graphs, which point into the old one."""
         if self._gemm_ws.numel() < nbytes:
+            self._prefill_graphs.clear()
             self._gemm_ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return self._gemm_ws
 
@@ -421,10 +424,16 @@ class LlamaHIP:
             self._prefill_bufs[S] = b
         return b
 
-    def prefill(self, token_ids) -> None:
+    def prefill(self, token_ids, use_graph: bool = False) -> None:
         """Process the prompt at positions pos..pos+S-1; leaves logits of the last
-        position in self.logits and the greedy next token in self.token."""
-        cfg, s = self.cfg, self._stream()
+        position in self.logits and the greedy next token in self.token.
+
+        With ``use_graph`` the launches run as a hipGraph captured once per
+        (prompt length, start position) -- after one eager run of that shape --
+        and replayed afterwards, so the host issues one graph instead of ~150
+        kernels. Results are bit-identical to the eager path. Graphs are dropped
+        when the split-K workspace they point into is reallocated."""
+        cfg = self.cfg
         ids = torch.as_tensor(token_ids, dtype=torch.int32).reshape(-1)
         S = int(ids.numel())
         pos0 = self.host_pos
@@ -432,6 +441,22 @@ class LlamaHIP:
             raise ValueError(f"prompt of {S} tokens at position {pos0} does not fit the KV capacity {cfg.max_seq_len}")
         b = self._pbufs(S)
         b["ids"].copy_(ids)
+        key = (S, pos0)
+        graph = self._prefill_graphs.get(key) if use_graph else None
+        if graph is not None:
+            graph.replay()
+        else:
+            self._prefill_launches(S, pos0)  # also sizes the workspace the capture will use
+            if use_graph:
+                self._prefill_graphs[key] = capture_graph(lambda: self._prefill_launches(S, pos0), self.device)
+        self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
+        self.host_pos = pos0 + S
+
+    def _prefill_launches(self, S: int, pos0: int) -> None:
+        """Every kernel of one prefill of S tokens at pos0 (token ids already in the
+        prefill buffer), on the current stream; capturable."""
+        cfg, s = self.cfg, self._stream()
+        b = self._pbufs(S)
         E, Hd = cfg.emb_dim, cfg.head_dim
         X, Xn, T = b["X"], b["Xn"], b["T"]
         _lib.call("iron_embedding", self.embed.data_ptr(), b["ids"].data_ptr(), X.data_ptr(), S, E, cfg.vocab_size, s)
@@ -482,8 +507,6 @@ class LlamaHIP:
             pending = linear(L["down"], b["G"], T)
         add_norm(pending)
         self.head.gemv(Xn[S - 1], self.logits, s, keys=self.keys)
-        self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
-        self.host_pos = pos0 + S
 
     def set_token(self, token: int) -> None:
         """Force the next input token (teacher forcing): the next step's selection

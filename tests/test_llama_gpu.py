@@ -169,3 +169,52 @@ def test_prefill_fused_merge_bit_identical(gpu, prefill_int4):
         for i in range(cfg.n_layers):
             assert torch.equal(fused.k_cache[i], plain.k_cache[i])
             assert torch.equal(fused.v_cache[i], plain.v_cache[i])
+
+
+def test_prefill_graph_matches_eager(gpu):
+    """prefill(use_graph=True): the first call of a (length, start) shape runs
+    eagerly and captures it, later calls replay the graph. Logits, KV caches and
+    the decode that follows must equal the eager path bit for bit, also after a
+    longer prompt grows the split-K workspace (which drops the old graphs)."""
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
+
+    cfg = LlamaConfig(**MID)
+    w = random_weights(cfg, gpu, seed=6)
+    gm, em = LlamaHIP(cfg, w, device=gpu), LlamaHIP(cfg, w, device=gpu)
+    g = torch.Generator().manual_seed(7)
+    p1 = torch.randint(0, cfg.vocab_size, (64,), generator=g).tolist()
+    p2 = torch.randint(0, cfg.vocab_size, (7,), generator=g).tolist()
+    long = torch.randint(0, cfg.vocab_size, (300,), generator=g).tolist()
+
+    def same():
+        torch.cuda.synchronize()
+        assert torch.equal(gm.logits, em.logits)
+        for i in range(cfg.n_layers):
+            assert torch.equal(gm.k_cache[i], em.k_cache[i]) and torch.equal(gm.v_cache[i], em.v_cache[i])
+
+    for rnd in range(2):  # round 0 captures, round 1 replays
+        for m in (gm, em):
+            m.reset()
+        gm.prefill(p1, use_graph=True)
+        em.prefill(p1)
+        same()
+        gm.prefill(p2, use_graph=True)  # continuation at position 64
+        em.prefill(p2)
+        same()
+        assert set(gm._prefill_graphs) == {(64, 0), (7, 64)}
+    for m in (gm, em):
+        m.decode(3)
+    same()
+    for m in (gm, em):
+        m.reset()
+    gm.prefill(long, use_graph=True)  # grows the workspace: earlier graphs are dropped
+    em.prefill(long)
+    same()
+    assert set(gm._prefill_graphs) == {(300, 0)}
+    for m in (gm, em):
+        m.reset()
+    gm.prefill(p1, use_graph=True)
+    gm.prefill(p1[:5], use_graph=True)
+    em.prefill(p1)
+    em.prefill(p1[:5])
+    same()
