@@ -30,6 +30,9 @@ beside the GPU decode rate in ``extra.llama_cfg5``. ``extra`` carries the other 
 configurations: bf16 GEMV (cfg 1), GQA decode (cfg 3), SwiGLU block bf16 and
 int4 (cfg 4), the prefill GEMM and the Llama-3.2-1B-shaped model (cfg 5:
 prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096 window).
+Its ``ttft_ms`` replays the prefill graph captured beforehand for the prompt
+length (``ttft_eager_ms``: the same prefill issued kernel by kernel); the
+token ids are copied from the host inside both timings.
 """
 
 from __future__ import annotations
