@@ -230,6 +230,8 @@ class Linear:
 class LlamaHIP:
     """Llama-3.2-1B-shaped model on one GPU: weights, KV caches and the decode graph."""
 
+    MAX_PREFILL_GRAPHS = 16  # captured prefill shapes kept at once (oldest dropped first)
+
     def __init__(self, cfg: LlamaConfig, weights: dict, device=None):
         cfg.validate()
         self.cfg = cfg
@@ -448,6 +450,8 @@ class LlamaHIP:
         else:
             self._prefill_launches(S, pos0)  # also sizes the workspace the capture will use
             if use_graph:
+                while self._prefill_graphs and len(self._prefill_graphs) >= self.MAX_PREFILL_GRAPHS:
+                    self._prefill_graphs.pop(next(iter(self._prefill_graphs)))  # the oldest shape first
                 self._prefill_graphs[key] = capture_graph(lambda: self._prefill_launches(S, pos0), self.device)
         self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
         self.host_pos = pos0 + S

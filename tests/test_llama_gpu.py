@@ -218,3 +218,8 @@ def test_prefill_graph_matches_eager(gpu):
     em.prefill(p1)
     em.prefill(p1[:5])
     same()
+    # at most MAX_PREFILL_GRAPHS shapes are kept, the oldest dropped first
+    gm.MAX_PREFILL_GRAPHS = 2
+    gm.reset()
+    gm.prefill(p1[:9], use_graph=True)
+    assert list(gm._prefill_graphs) == [(5, 64), (9, 0)]
