@@ -60,8 +60,22 @@ METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 TRAFFIC_BYTES = 9551129
 
 
+def copies_for(nbytes: int) -> int:
+    """Distinct copies of an nbytes working set that fill the rotation pool."""
+    return max(2, -(-POOL_BYTES // nbytes))
+
+
 class Timer:
-    """Device time of launch closures launch(i, stream): hipGraph replays, or calls issued one at a time."""
+    """Device time of launch closures launch(i, stream), where launch i reads copy
+    i % copies of its inputs.
+
+    Cache-proof protocol: a launch never re-reads a copy until every other copy
+    (>= POOL_BYTES of distinct data in all) has been read since, so the 256 MiB
+    Infinity Cache cannot serve the timed launches at any step count. Graphs
+    hold a multiple of `copies` consecutive launches (each replay reads every
+    copy once, in order), and a warm replay of the full rotation precedes every
+    timed region.
+    """
 
     def __init__(self, torch, lib):
         self.torch, self.lib = torch, lib
@@ -80,24 +94,32 @@ class Timer:
 
         return capture_graph(body, dev)
 
-    def graph_ms(self, graph, replays):
-        """Events around `replays` back-to-back replays of `graph` on the current stream (milliseconds)."""
+    def replay_ms(self, graphs, lead=None):
+        """Events (on the replay stream) around back-to-back replays of `graphs`, in
+        order (milliseconds). `lead`, replayed first and untimed, keeps the GPU
+        busy while the host submits the timed graphs, so the start event is
+        recorded when the lead ends, with the timed graphs already queued: the
+        host's graph-launch latency stays out of the timed region."""
         torch = self.torch
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        if lead is not None:
+            lead.replay()
         a.record()
-        for _ in range(replays):
-            graph.replay()
+        for g in graphs:
+            g.replay()
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b)
 
-    def graph_us(self, launch, n, rounds=5):
-        """Device time per launch(i, stream): n consecutive launches captured in one
-        hipGraph, replayed back to back; median over `rounds` replays (microseconds)."""
+    def rotating_us(self, launch, copies, min_launches=200, rounds=5):
+        """Device time per launch (microseconds): a graph of n consecutive launches,
+        n the smallest multiple of `copies` >= min_launches; each round replays it
+        once untimed (the lead) and once timed; the median over `rounds`."""
+        n = copies * max(1, -(-min_launches // copies))
         g = self.capture(launch, n)
         g.replay()
-        t = sorted(self.graph_ms(g, 1) * 1e3 / n for _ in range(rounds))
+        t = sorted(self.replay_ms([g], lead=g) * 1e3 / n for _ in range(rounds))
         del g
         return t[len(t) // 2]
 
@@ -117,19 +139,50 @@ class Timer:
         return a.elapsed_time(b)
 
 
+def metric_lines(name, latency_us, nbytes):
+    """The per-operator lines the reference's operator tests print and its CI
+    scrapes (iron/common/test_utils.py:293-294), on stderr so that stdout
+    stays the one JSON line."""
+    print(f"[{name}]\nLatency (us): {latency_us:.1f}\nEffective Bandwidth: {nbytes / (latency_us * 1e-6) / 1e9:.6e} GB/s",
+          file=sys.stderr, flush=True)
+
+
+def cpu_time(fn, budget_s):
+    """fn() timed on the host: one warm call, then repeated calls until budget_s
+    is spent (at least one). Returns (calls, seconds)."""
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < budget_s:
+        fn()
+        reps += 1
+    return reps, time.perf_counter() - t0
+
+
+def cpu_threads(torch) -> int:
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    return threads
+
+
 def _check(lib, rc):
     if rc:
         raise RuntimeError(lib.iron_last_error().decode())
 
 
 def bench_gemv_int4(torch, lib, tm, dev, steps, warmup):
+    """The headline: `steps` launches of the config 2 GEMV, timed as graph replays
+    that follow the cache-proof rotation (Timer): a graph G of one launch per
+    weight copy (every copy once, in order) is replayed once warm, then the
+    timed region is q replays of G plus one graph of the remaining r launches
+    (steps = q * copies + r), so every timed launch reads a copy that
+    `copies - 1` other launches (>= POOL_BYTES) have read past since its last use."""
     from iron_amd import _lib
     from oracle import configs
 
     M, K = 8192, 2048
     codes, scales, x = configs.cfg2_gemv_int4(M=M, K=K)
     nbytes = M * K // 2 + 2 * M * K // 32 + 2 * K + 2 * M
-    copies = max(2, POOL_BYTES // (codes.numel() + 2 * scales.numel()))
+    copies = copies_for(codes.numel() + 2 * scales.numel())
     C = [codes.to(dev) for _ in range(copies)]
     S = [scales.to(dev) for _ in range(copies)]
     xd = x.to(dev)
@@ -144,27 +197,57 @@ def bench_gemv_int4(torch, lib, tm, dev, steps, warmup):
 
     for i in range(warmup):
         launch(i, stream)
-    # the timed steps: replays of a graph of `chunk` consecutive launches
-    chunk = max(d for d in range(1, min(steps, 100) + 1) if steps % d == 0)
-    graph = tm.capture(launch, chunk)
-    graph.replay()
-    wall = tm.graph_ms(graph, steps // chunk)
-    del graph
+    full = tm.capture(launch, copies)
+    q, r = divmod(steps, copies)
+    tail = tm.capture(launch, r) if r else None
+    full.replay()
+    # timed: q replays of the full rotation + the tail, after an untimed lead
+    # replay of the full rotation (every copy read once, in order)
+    wall = tm.replay_ms([full] * q + ([tail] if tail else []), lead=full)
+    del full, tail
     # the same kernel issued one Python call at a time (host-bound when the kernel is short)
     n_py = min(steps, 1000)
     py_us = tm.wall_ms(launch, n_py) * 1e3 / n_py
-    return {"bytes": nbytes, "wall_ms": wall, "chunk": chunk, "python_launch_us": py_us, "copies": copies,
+    return {"bytes": nbytes, "wall_ms": wall, "copies": copies, "python_launch_us": py_us,
+            "launches_per_graph": copies, "tail_launches": r,
+            "timed_distinct_bytes": min(steps, copies) * (codes.numel() + 2 * scales.numel()),
             "inputs": (codes, scales, x)}
 
 
-def bench_gemv_bf16(torch, lib, tm, dev, n):
+def _gpu_line(name, kern_us, nbytes=None, flops=None, cpu=None):
+    """One config's GPU figure (HBM GB/s or MFMA TFLOP/s) with its CPU baseline beside it."""
+    out = {"kernel_us": round(kern_us, 3)}
+    if nbytes is not None:
+        out.update({"GB/s": round(nbytes / kern_us / 1e3, 1), "frac_hbm": round(nbytes / kern_us / 1e3 / HBM_PEAK_GBS, 4),
+                    "algorithmic_bytes": nbytes})
+        metric_lines(name, kern_us, nbytes)
+    if flops is not None:
+        tf = flops / kern_us / 1e6
+        out.update({"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4), "flops": int(flops)})
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    return out
+
+
+def _cpu_line(torch, fn, budget_s, unit_work, unit, what):
+    """CPU baseline of one config: fn() on the host cores for ~budget_s seconds;
+    value = unit_work per call x calls / seconds (unit_work in GB or TFLOP)."""
+    if budget_s <= 0:
+        return None
+    threads = cpu_threads(torch)
+    reps, dt = cpu_time(fn, budget_s)
+    return {"value": round(unit_work * reps / dt, 4), "unit": unit, "cores": threads, "kind": "port",
+            "sample": f"{reps} x {what}, {dt:.1f} s"}
+
+
+def bench_gemv_bf16(torch, lib, tm, dev, n, cpu_s=0.0):
     from iron_amd import _lib
-    from oracle import configs
+    from oracle import configs, ops
 
     M, K = 2048, 8192
     W, x = configs.cfg1_gemv_bf16(M=M, K=K)
     nbytes = 2 * M * K + 2 * K + 2 * M
-    copies = max(2, POOL_BYTES // (2 * W.numel()))
+    copies = copies_for(2 * W.numel())
     Ws = [W.to(dev) for _ in range(copies)]
     xd = x.to(dev)
     y = torch.empty(M, dtype=torch.bfloat16, device=dev)
@@ -175,45 +258,61 @@ def bench_gemv_bf16(torch, lib, tm, dev, n):
 
     for i in range(20):
         launch(i, stream)
-    kern = tm.graph_us(launch, n)
+    kern = tm.rotating_us(launch, copies, n)
     b2b = tm.wall_ms(launch, n) * 1e3 / n
-    return {"kernel_us": round(kern, 3), "GB/s": round(nbytes / kern / 1e3, 1),
-            "frac_hbm": round(nbytes / kern / 1e3 / HBM_PEAK_GBS, 4), "python_launch_us": round(b2b, 3),
-            "algorithmic_bytes": nbytes}
+    cpu = _cpu_line(torch, lambda: ops.gemv_reference(W, x), cpu_s, nbytes / 1e9, "GB/s",
+                    "config-1 bf16 GEMV (2048x8192) via oracle.ops.gemv_reference (torch CPU, fp32 matvec)")
+    out = _gpu_line("gemv_bf16_cfg1", kern, nbytes=nbytes, cpu=cpu)
+    out["python_launch_us"] = round(b2b, 3)
+    out["weight_copies"] = copies
+    return out
 
 
-def bench_gqa(torch, lib, tm, dev, n):
+def bench_gqa(torch, lib, tm, dev, n, L=2048, max_len=None, cpu_s=0.0):
+    """GQA decode attention (32/8 heads, d 64) with the new token at position
+    L-1 of a cache of capacity max_len (config 3: L = max_len = 2048)."""
     from iron_amd import _lib
-    from oracle import configs
+    from oracle import configs, ops
 
-    H, Hkv, D, L = 32, 8, 64, 2048
+    H, Hkv, D = 32, 8, 64
+    max_len = max_len or L
     q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, head_dim=D, L=L)
+    if max_len > L:
+        pad = torch.zeros(Hkv, max_len - L, D, dtype=kc.dtype)
+        kc, vc = torch.cat([kc, pad], 1), torch.cat([vc, pad], 1)
+        angles = ops.rope_angles_table(D, max_len, theta=500000.0)
     nbytes = 2 * Hkv * L * D * 2 + H * D * 2 * 2 + 2 * Hkv * D * 2 + D * 4
-    copies = max(2, POOL_BYTES // (2 * kc.numel() * 2))
+    copies = copies_for(2 * Hkv * L * D * 2)
     KC = [kc.to(dev) for _ in range(copies)]
     VC = [vc.to(dev) for _ in range(copies)]
     qd, knd, vnd, ad = q.to(dev), kn.to(dev), vn.to(dev), angles.to(dev)
     out = torch.empty(H, D, dtype=torch.bfloat16, device=dev)
-    ws = torch.zeros(int(lib.iron_gqa_decode_workspace_bytes(H, Hkv, D, L)), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(int(lib.iron_gqa_decode_workspace_bytes(H, Hkv, D, max_len)), dtype=torch.uint8, device=dev)
     stream = _lib.stream_handle(dev)
 
     def launch(i, s):
         _check(lib, lib.iron_gqa_decode(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), KC[i % copies].data_ptr(),
-                                        VC[i % copies].data_ptr(), ad.data_ptr(), L, out.data_ptr(), ws.data_ptr(),
-                                        H, Hkv, D, L, pos, None, 1.0 / math.sqrt(D), s))
+                                        VC[i % copies].data_ptr(), ad.data_ptr(), angles.shape[0], out.data_ptr(),
+                                        ws.data_ptr(), H, Hkv, D, max_len, pos, None, 1.0 / math.sqrt(D), s))
 
     for i in range(20):
         launch(i, stream)
-    kern = tm.graph_us(launch, n)
-    return {"kernel_us": round(kern, 3), "GB/s": round(nbytes / kern / 1e3, 1),
-            "frac_hbm": round(nbytes / kern / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    kern = tm.rotating_us(launch, copies, n)
+    cpu = None
+    if cpu_s > 0:
+        cpu = _cpu_line(torch, lambda: ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles, scale=1.0 / math.sqrt(D)),
+                        cpu_s, nbytes / 1e9, "GB/s",
+                        f"GQA decode at KV {L} via oracle.ops.gqa_decode_reference (torch CPU, fp32 softmax attention)")
+    res = _gpu_line(f"gqa_decode_L{L}", kern, nbytes=nbytes, cpu=cpu)
+    res.update({"kv_len": L, "max_len": max_len, "cache_copies": copies})
+    return res
 
 
-def bench_swiglu(torch, lib, tm, dev, n):
+def bench_swiglu(torch, lib, tm, dev, n, cpu_s=0.0):
     """Config 4: x + Wd(silu(Wg xn) * (Wu xn)), xn = RMSNorm(x)*w: two kernels
     (norm + gate/up pair GEMV, then down GEMV + residual)."""
     from iron_amd import _lib
-    from oracle import configs
+    from oracle import configs, ops
 
     E, F = 2048, 8192
     x, nw, Wg, Wu, Wd = configs.cfg4_swiglu_block(E, F)
@@ -224,7 +323,7 @@ def bench_swiglu(torch, lib, tm, dev, n):
     res = {}
     # bf16
     g_, u_, d_ = Wg.to(dev), Wu.to(dev), Wd.to(dev)
-    reps = max(2, POOL_BYTES // (3 * 2 * E * F))
+    reps = copies_for(3 * 2 * E * F)
     G = [g_] + [g_.clone() for _ in range(reps - 1)]
     U = [u_] + [u_.clone() for _ in range(reps - 1)]
     Dn = [d_] + [d_.clone() for _ in range(reps - 1)]
@@ -237,10 +336,11 @@ def bench_swiglu(torch, lib, tm, dev, n):
 
     for i in range(10):
         block(i, stream)
-    t = tm.graph_us(block, n)
+    t = tm.rotating_us(block, reps, n)
     nbytes = 3 * 2 * E * F + 4 * E + 2 * 2 * F + 2 * E * 2
-    res["bf16"] = {"kernel_us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1),
-                   "frac_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    cpu = _cpu_line(torch, lambda: ops.swiglu_block_reference(x, nw, Wg, Wu, Wd), cpu_s, nbytes / 1e9, "GB/s",
+                    "config-4 bf16 SwiGLU block via oracle.ops.swiglu_block_reference (torch CPU)")
+    res["bf16"] = _gpu_line("swiglu_block_bf16_cfg4", t, nbytes=nbytes, cpu=cpu)
     del G, U, Dn
     # int4-g32
     q = {}
@@ -252,7 +352,7 @@ def bench_swiglu(torch, lib, tm, dev, n):
                                             stream))
         q[name] = (c, s)
     per = sum(c.numel() + 2 * s.numel() for c, s in q.values())
-    reps = max(2, POOL_BYTES // per)
+    reps = copies_for(per)
     Q = [q] + [{k: (c.clone(), s.clone()) for k, (c, s) in q.items()} for _ in range(reps - 1)]
 
     def block4(i, s):
@@ -265,17 +365,28 @@ def bench_swiglu(torch, lib, tm, dev, n):
 
     for i in range(10):
         block4(i, stream)
-    t = tm.graph_us(block4, n)
+    t = tm.rotating_us(block4, reps, n)
     nbytes = per + 4 * E + 2 * 2 * F + 2 * E * 2
-    res["int4_g32"] = {"kernel_us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1),
-                       "frac_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    cpu = None
+    if cpu_s > 0:
+        host = {k: (c.cpu(), s.cpu()) for k, (c, s) in q.items()}
+
+        def cpu_block4():
+            Wq = {k: ops.dequant_planar(c, s) for k, (c, s) in host.items()}
+            return ops.swiglu_block_reference(x, nw, Wq["g"], Wq["u"], Wq["d"])
+
+        cpu = _cpu_line(torch, cpu_block4, cpu_s, nbytes / 1e9, "GB/s",
+                        "config-4 int4-g32 SwiGLU block (oracle.ops.dequant_planar, then swiglu_block_reference)")
+    res["int4_g32"] = _gpu_line("swiglu_block_int4_cfg4", t, nbytes=nbytes, cpu=cpu)
     return res
 
 
-def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False):
+def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0):
     """Config 5 prefill GEMM M=512 K=2048 N=8192 (bf16 weights, or int4-g32
-    weights dequantised in the kernel's prologue)."""
+    weights dequantised in the kernel's prologue), weights rotated through the
+    pool (cold, as in the model, where each layer's weights are read once)."""
     from iron_amd import _lib
+    from oracle import ops
 
     M, K, N = 512, 2048, 8192
     g = torch.Generator(device=dev).manual_seed(0)
@@ -287,26 +398,39 @@ def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False):
         codes = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
         scales = torch.empty(N, K // 32, dtype=torch.bfloat16, device=dev)
         _check(lib, lib.iron_quantize_i4g32(W.data_ptr(), codes.data_ptr(), scales.data_ptr(), N, K, stream))
+        copies = copies_for(codes.numel() + 2 * scales.numel())
+        CS = [(codes, scales)] + [(codes.clone(), scales.clone()) for _ in range(copies - 1)]
+    else:
+        copies = copies_for(2 * W.numel())
+        Ws = [W] + [W.clone() for _ in range(copies - 1)]
 
     def launch(i, s):
         if int4:
-            _check(lib, lib.iron_gemm_i4g32_nt(A.data_ptr(), codes.data_ptr(), scales.data_ptr(), C.data_ptr(), M, N,
+            c, sc = CS[i % copies]
+            _check(lib, lib.iron_gemm_i4g32_nt(A.data_ptr(), c.data_ptr(), sc.data_ptr(), C.data_ptr(), M, N,
                                                K, N, 0, 0, 0.0, 0.0, 1, 1, None, 0, s))
         else:
-            _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
-                                              s))
+            _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), Ws[i % copies].data_ptr(), C.data_ptr(), M, N, K, N, 0,
+                                              0, 0.0, 0.0, s))
 
     for i in range(10):
         launch(i, stream)
-    t = tm.graph_us(launch, n)
-    tf = 2.0 * M * N * K / t / 1e6
-    return {"shape": [M, K, N], "weights": "int4-g32" if int4 else "bf16", "kernel_us": round(t, 3),
-            "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+    t = tm.rotating_us(launch, copies, n)
+    cpu = None
+    if cpu_s > 0 and not int4:
+        Ah, Wh = A.cpu(), W.cpu()
+        cpu = _cpu_line(torch, lambda: ops.gemm_reference(Ah, Wh, b_col_maj=True), cpu_s, 2.0 * M * N * K / 1e12,
+                        "TFLOP/s", "config-5 prefill GEMM 512x2048x8192 via oracle.ops.gemm_reference (torch CPU, fp32)")
+    res = _gpu_line("prefill_gemm" + ("_int4" if int4 else ""), t, flops=2.0 * M * N * K, cpu=cpu)
+    res.update({"shape": [M, K, N], "weights": "int4-g32" if int4 else "bf16", "weight_copies": copies})
+    return res
 
 
 def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
     """Causal GQA prefill attention of cfg 5's long prompt (32/8 heads, d 64):
-    useful flops 4 * S * (S + 1) / 2 * d per head (QK^T and PV, visible keys)."""
+    useful flops 4 * S * (S + 1) / 2 * d per head (QK^T and PV, visible keys).
+    The 24 MB of operands are re-read many times per launch by design, so they
+    are not rotated."""
     from iron_amd import _lib
 
     H, Hkv, D = 32, 8, 64
@@ -323,10 +447,52 @@ def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
 
     for i in range(5):
         launch(i, stream)
-    t = tm.graph_us(launch, n)
-    flops = 4.0 * S * (S + 1) / 2 * D * H
-    tf = flops / t / 1e6
-    return {"seq": S, "kernel_us": round(t, 3), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+    t = tm.rotating_us(launch, 1, n)
+    res = _gpu_line("prefill_attention", t, flops=4.0 * S * (S + 1) / 2 * D * H)
+    res["seq"] = S
+    return res
+
+
+def bench_floor(torch, lib, tm, dev):
+    """The floors that bound one short launch, measured with the protocol of the
+    kernels they bound: an empty kernel as one node of a replayed graph (and
+    issued one Python call at a time), and a pure streaming read of the decode
+    kernels' sizes from the rotation pool, at 1..8 16-byte loads in flight per
+    lane (iron_probe_read)."""
+    from iron_amd import _lib
+
+    out = {"empty_graph_node_us": {}, "empty_python_launch_us": {}, "read_us": {}}
+    for wgs in (1, 256, 2048, 8192):
+        def empty(i, s, wgs=wgs):
+            _check(lib, lib.iron_probe_empty(wgs, s))
+
+        empty(0, _lib.stream_handle(dev))
+        out["empty_graph_node_us"][str(wgs)] = round(tm.rotating_us(empty, 1, 500), 3)
+        out["empty_python_launch_us"][str(wgs)] = round(tm.wall_ms(empty, 500) * 1e3 / 500, 3)
+    sizes = {"cfg2_int4_gemv": 9457664, "cfg3_gqa_kv": 4194304, "kv4096_layer": 8388608,
+             "cfg1_bf16_gemv": 33574912}
+    for name, nbytes in sizes.items():
+        stride = (nbytes + 255) // 256 * 256
+        copies = copies_for(stride)
+        pool = torch.empty(copies * stride, dtype=torch.uint8, device=dev)
+        pool.random_(0, 256)
+        base = pool.data_ptr()
+        row = {}
+        for lpl in (1, 2, 4, 8):
+            wgs = int(lib.iron_probe_read_workgroups(nbytes, lpl))
+            sink = torch.empty(wgs, dtype=torch.int32, device=dev)
+
+            def read(i, s, lpl=lpl, sink=sink, wgs=wgs):
+                _check(lib, lib.iron_probe_read(base + (i % copies) * stride, nbytes, sink.data_ptr(), wgs, lpl, s))
+
+            read(0, _lib.stream_handle(dev))
+            t = tm.rotating_us(read, copies, 200)
+            row[f"loads_per_lane_{lpl}"] = {"us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1)}
+        best = min(v["us"] for v in row.values())
+        out["read_us"][name] = {"bytes": nbytes, "best_us": best, "best_GB/s": round(nbytes / best / 1e3, 1),
+                                "by_shape": row}
+        del pool
+    return out
 
 
 def bench_model(torch, dev, decode_steps=128, prompt_len=512, long_ctx=3968):
@@ -487,8 +653,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill"], default="full")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
+                    "baselines get a third of it each)")
+    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill", "attention", "floor"], default="full")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -510,27 +678,31 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     tm = Timer(torch, lib)
 
+    def emit(mode, extra):
+        print(json.dumps({"metric": METRIC, "mode": mode, "extra": extra}), flush=True)
+        return 0
+
     if args.mode == "model":
-        out = {"metric": METRIC, "mode": "model", "extra": {"llama_cfg5": bench_model(torch, dev)}}
-        print(json.dumps(out), flush=True)
-        return 0
+        return emit("model", {"llama_cfg5": bench_model(torch, dev)})
     if args.mode == "prefill":
-        out = {
-            "metric": METRIC,
-            "mode": "prefill",
-            "extra": {
-                "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
-                "prefill_gemm_int4_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, int4=True),
-                "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
-            },
-        }
-        print(json.dumps(out), flush=True)
-        return 0
+        return emit("prefill", {
+            "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+            "prefill_gemm_int4_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, int4=True),
+            "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
+        })
+    if args.mode == "attention":
+        return emit("attention", {
+            "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
+            "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608),
+        })
+    if args.mode == "floor":
+        return emit("floor", {"floor": bench_floor(torch, lib, tm, dev)})
 
     i4 = bench_gemv_int4(torch, lib, tm, dev, args.steps, args.warmup)
     value = i4["bytes"] * args.steps / (i4["wall_ms"] * 1e-3) / 1e9
     kernel_us = i4["wall_ms"] * 1e3 / args.steps
     achieved = i4["bytes"] / kernel_us / 1e3
+    metric_lines("gemv_int4_cfg2", kernel_us, i4["bytes"])
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -549,7 +721,9 @@ def main() -> int:
             "codes, bf16 group-32 scales, zero-point 0), x 2048 bf16 ~N(0,1), fp32 accumulate, bf16 out, seed 0",
             "weight_pool_copies": i4["copies"],
             "algorithmic_bytes_per_step": i4["bytes"],
-            "launches_per_graph_replay": i4["chunk"],
+            "timed_distinct_bytes": i4["timed_distinct_bytes"],
+            "launches_per_graph_replay": i4["launches_per_graph"],
+            "tail_graph_launches": i4["tail_launches"],
             "python_launch_us": round(i4["python_launch_us"], 3),
         },
         "roofline": {
@@ -571,11 +745,13 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
     else:
+        cs = 0.0 if args.no_cpu_baseline else args.cpu_seconds / 3
         extra = {
-            "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300),
-            "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
-            "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200),
-            "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100),
+            "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300, cpu_s=cs),
+            "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300, cpu_s=cs),
+            "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608),
+            "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200, cpu_s=cs),
+            "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, cpu_s=cs),
             "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
             "llama_cfg5": bench_model(torch, dev),
         }

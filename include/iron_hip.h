@@ -350,6 +350,23 @@ int iron_qkv_rope_scatter_splitk(const float* partial, int splits, const float* 
                                  void* k_cache, void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim,
                                  int max_len, int pos0, void* stream);
 
+/* -------------------------------------------------- Measurement probes ---- */
+/* No counterpart in the reference: they measure the floors that bound the
+ * short decode kernels (bench.py --mode floor). */
+
+/* An empty kernel of `workgroups` x 256 threads: the cost of one launch. */
+int iron_probe_empty(int workgroups, void* stream);
+
+/* Workgroups iron_probe_read launches for this size (-1 if invalid). */
+long long iron_probe_read_workgroups(long long nbytes, int loads_per_lane);
+
+/* Reads nbytes (a multiple of 16, src 16-byte aligned) with 16-byte
+ * nontemporal loads, loads_per_lane in {1,2,4,8} in flight per lane, and
+ * writes one XOR word per workgroup to sink (sink_words >= the count above):
+ * the cost of streaming that many bytes in one launch. */
+int iron_probe_read(const void* src, long long nbytes, void* sink, long long sink_words, int loads_per_lane,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, list] = {
     "iron_qkv_rope_scatter_splitk": [_P, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "iron_rmsnorm_splitk": [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P],
     "iron_gemm_nt_partials": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _LL, _P],
+    "iron_probe_empty": [_I, _P],
+    "iron_probe_read": [_P, _LL, _P, _LL, _I, _P],
 }
 
 # ... except these queries, which return a value.
@@ -64,6 +66,7 @@ QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
+    "iron_probe_read_workgroups": (_LL, [_LL, _I]),
 }
 
 _lock = threading.Lock()

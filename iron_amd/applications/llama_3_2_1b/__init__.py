@@ -12,10 +12,12 @@ from .harness import (
     hip_forward_pass,
     init,
     load_safetensors_weights,
+    get_model_reference,
+    set_model_reference,
 )
 
 __all__ = [
     "LlamaConfig", "LlamaHIP", "compute_rope_angles", "random_weights", "HarnessConfig", "LlamaModelState",
     "check_accuracy", "check_determinism", "config_from_weights", "generate", "generate_token", "hip_forward_pass",
-    "init", "load_safetensors_weights",
+    "init", "load_safetensors_weights", "get_model_reference", "set_model_reference",
 ]

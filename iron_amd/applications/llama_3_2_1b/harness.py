@@ -9,9 +9,10 @@ returns ``(logits (1, n, vocab), state)``.
 - ``generate``: prefill + decode loop, printing tokens and the TTFT / tokens
   per second statistics (harness:298-348); returns the tokens and the stats.
 - ``check_accuracy``: teacher-forced KL(reference || candidate) and top-1
-  agreement per step against another forward pass (harness:172-198).
-- ``check_determinism``: alternating prompts, logits compared bitwise
-  (harness:201-228).
+  agreement per step against another forward pass (the gate of
+  harness:172-198; same signature and return value).
+- ``check_determinism``: alternating prompts, logits compared bitwise (the
+  gate of harness:201-228; same signature and return value).
 
 ``hip_forward_pass`` runs the model: a state with more than one token id (or
 an empty cache) prefills, a single token id decodes one step (captured graph).
@@ -151,50 +152,88 @@ def generate(config, state, forward_pass=hip_forward_pass, num_tokens=100, use_k
     return tokens, stats
 
 
+def _divergence(ref_logits: torch.Tensor, cand_logits: torch.Tensor):
+    """(KL(ref || cand), top-1 agreement, the reference's greedy token) of two
+    next-token logit vectors, in float64."""
+    ref_lp = torch.log_softmax(ref_logits.reshape(-1).double(), dim=0)
+    cand_lp = torch.log_softmax(cand_logits.reshape(-1).double(), dim=0)
+    kl = torch.nn.functional.kl_div(cand_lp, ref_lp, reduction="sum", log_target=True)
+    want = int(torch.argmax(ref_lp))
+    return float(kl), int(torch.argmax(cand_lp)) == want, want
+
+
 def check_accuracy(config, state, forward_pass, ref_config, ref_state, ref_forward_pass, num_tokens):
-    """Teacher-forced per-step (KL(reference || candidate), top-1 match);
-    step 0 is prefill (harness:172-198)."""
+    """Teacher-forced comparison against a reference forward pass
+    (the gate of llama_inference_harness.py:172-198).
+
+    Both passes start from ``state.token_ids``; after every step both are fed
+    the reference's greedy token, so step n measures the candidate's own error
+    at step n. Step 0 is the prefill. Returns one ``(kl, top1)`` per step:
+    KL(reference || candidate) of the next-token distributions and whether
+    both put the same token first.
+    """
     ref_state.token_ids = state.token_ids
     results = []
     for step in range(num_tokens):
-        logits, state = forward_pass(config, state)
-        ref_logits, ref_state = ref_forward_pass(ref_config, ref_state)
-        cand = torch.log_softmax(logits[0, -1].float(), dim=0)
-        ref = torch.log_softmax(ref_logits[0, -1].float(), dim=0)
-        kl = torch.sum(ref.exp() * (ref - cand)).item()
-        nxt = int(ref.argmax())
-        top1 = int(cand.argmax()) == nxt
-        results.append((kl, top1))
-        print(f"step {step:3d}  KL {kl:.5f}  top-1 {'match' if top1 else 'MISMATCH'}")
-        state.token_ids = torch.tensor([[nxt]], dtype=torch.long)
-        ref_state.token_ids = state.token_ids
+        cand, state = forward_pass(config, state)
+        ref, ref_state = ref_forward_pass(ref_config, ref_state)
+        kl, same, forced = _divergence(ref[0, -1], cand[0, -1])
+        results.append((kl, same))
+        print(f"[step {step}] KL(ref||cand) = {kl:.3e}, top-1 {'agrees' if same else 'DIFFERS'}", flush=True)
+        state.token_ids = ref_state.token_ids = torch.full((1, 1), forced, dtype=torch.long)
     return results
 
 
 def check_determinism(config, prompts, forward_pass, num_tokens, rounds, make_state=LlamaModelState):
-    """Each prompt ``rounds`` times, alternating, greedy; returns how many
-    rounds' logits differ bitwise from that prompt's first round
-    (harness:201-228)."""
-    first = [None] * len(prompts)
-    n_differ = 0
-    for r in range(rounds * len(prompts)):
-        p = r % len(prompts)
-        state = make_state(config)
-        state.token_ids = prompts[p]
-        logits = []
-        for _ in range(num_tokens):
-            out, state = forward_pass(config, state)
-            logits.append(out[0, -1].clone())
-            state.token_ids = out[:, -1:].argmax(dim=-1)
-        logits = torch.stack(logits).to(torch.bfloat16).view(torch.int16)
-        if first[p] is None:
-            first[p] = logits
-            continue
-        steps = (logits != first[p]).any(dim=1).nonzero().flatten().tolist()
-        if steps:
-            n_differ += 1
-            print(f"round {r} (prompt {p}): logits differ at steps {steps}")
-    return n_differ
+    """Bitwise reproducibility (the gate of llama_inference_harness.py:201-228).
+
+    Each round runs every prompt in turn (so consecutive runs alternate
+    prompts) from a fresh state, greedily, for ``num_tokens`` steps, and keeps
+    the bf16 bit patterns of each step's logits. Rounds after the first are
+    compared with the first round of the same prompt. Returns the number of
+    runs that differ anywhere.
+    """
+    baseline: dict[int, torch.Tensor] = {}
+    differing = 0
+    for rnd in range(rounds):
+        for p, prompt in enumerate(prompts):
+            state = make_state(config)
+            state.token_ids = prompt
+            bits = []
+            for _ in range(num_tokens):
+                logits, state = forward_pass(config, state)
+                last = logits[0, -1]
+                bits.append(last.to(torch.bfloat16).view(torch.int16))
+                state.token_ids = torch.argmax(last).reshape(1, 1)
+            run = torch.stack(bits)
+            if p not in baseline:
+                baseline[p] = run
+                continue
+            bad = torch.nonzero((run != baseline[p]).any(dim=1)).flatten().tolist()
+            if bad:
+                differing += 1
+                print(f"determinism: prompt {p}, round {rnd}: logits at steps {bad} differ from round 0", flush=True)
+    return differing
+
+
+# The CPU reference model that --check-accuracy compares against. The library
+# ships only the HIP path, so a caller registers one (the test suite registers
+# its fp32 oracle): factory(model) -> (ref_config, make_ref_state,
+# ref_forward_pass), where make_ref_state(ref_config) is a fresh reference
+# state and ref_forward_pass(ref_config, ref_state) returns (logits (1, n,
+# vocab), ref_state) for ref_state.token_ids, as forward_pass does.
+_model_reference = None
+
+
+def set_model_reference(factory) -> None:
+    """Register (or clear, with None) the reference-model factory used by the
+    accuracy check of the application entry point."""
+    global _model_reference
+    _model_reference = factory
+
+
+def get_model_reference():
+    return _model_reference
 
 
 def load_safetensors_weights(path, device="cpu") -> dict:

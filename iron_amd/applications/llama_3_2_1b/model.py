@@ -230,7 +230,7 @@ class Linear:
 class LlamaHIP:
     """Llama-3.2-1B-shaped model on one GPU: weights, KV caches and the decode graph."""
 
-    MAX_PREFILL_GRAPHS = 16  # captured prefill shapes kept at once (oldest dropped first)
+    MAX_PREFILL_GRAPHS = 16  # captured prefill shapes kept at once (least recently used dropped first)
 
     def __init__(self, cfg: LlamaConfig, weights: dict, device=None):
         cfg.validate()
@@ -293,8 +293,8 @@ class LlamaHIP:
         self.history = torch.zeros(L, dtype=torch.int32, device=dev)
         self.host_pos = 0
         self.graph = None
-        self._prefill_bufs = {}
-        self._prefill_graphs = {}  # (prompt length, start position) -> captured prefill
+        self._prefill_bufs = None  # activations of the longest prompt seen (see _pbufs)
+        self._prefill_graphs = {}  # (prompt length, start position) -> captured prefill, least recently used first
         self._gemm_ws = torch.empty(0, dtype=torch.uint8, device=dev)
         torch.cuda.synchronize(dev)
 
@@ -399,32 +399,45 @@ class LlamaHIP:
         self.host_pos += n_steps
 
     # ------------------------------------------------------------ prefill
+    def _drop_prefill_graphs(self) -> None:
+        """Forget every captured prefill graph, after the GPU has finished any
+        replay of them (destroying an executable graph while it runs is not
+        defined). Never called under capture: capture follows an eager run of
+        the same shape, which has already sized the workspace and buffers."""
+        if self._prefill_graphs:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("prefill buffers or workspace resized during graph capture")
+            torch.cuda.synchronize(self.device)
+            self._prefill_graphs.clear()
+
     def _workspace(self, nbytes: int) -> torch.Tensor:
         """Split-K GEMM workspace of at least ``nbytes`` (grown on demand; stream-ordered reuse).
         Growing it drops the captured prefill graphs, which point into the old one."""
         if self._gemm_ws.numel() < nbytes:
-            self._prefill_graphs.clear()
+            self._drop_prefill_graphs()
             self._gemm_ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return self._gemm_ws
 
     def _pbufs(self, S: int):
-        b = self._prefill_bufs.get(S)
-        if b is None:
+        """Prefill activations for S tokens: views of one set of buffers sized for
+        the longest prompt seen (rounded up to a power of two, at most the KV
+        capacity), so memory stays bounded by that prompt whatever lengths
+        come and go. Growing them drops the captured prefill graphs."""
+        b = self._prefill_bufs
+        if b is None or b["cap"] < S:
             cfg, dev = self.cfg, self.device
             E, Hd = cfg.emb_dim, cfg.head_dim
-            b = {
-                "ids": torch.zeros(S, dtype=torch.int32, device=dev),
-                "X": torch.zeros(S, E, dtype=BF16, device=dev),
-                "Xn": torch.zeros(S, E, dtype=BF16, device=dev),
-                "QKV": torch.zeros(S, cfg.qkv_dim, dtype=BF16, device=dev),
-                "Q": torch.zeros(S, cfg.n_heads * Hd, dtype=BF16, device=dev),
-                "O": torch.zeros(S, cfg.n_heads * Hd, dtype=BF16, device=dev),
-                "T": torch.zeros(S, E, dtype=BF16, device=dev),
-                "G": torch.zeros(S, cfg.hidden_dim, dtype=BF16, device=dev),
-                "U": torch.zeros(S, cfg.hidden_dim, dtype=BF16, device=dev),
-            }
-            self._prefill_bufs[S] = b
-        return b
+            cap = min(max(64, 1 << (S - 1).bit_length()), max(S, cfg.max_seq_len))
+            self._drop_prefill_graphs()
+            self._prefill_bufs = None  # release the old set before allocating the new one
+            b = {"cap": cap}
+            for name, cols, dt in (("ids", 0, torch.int32), ("X", E, BF16), ("Xn", E, BF16),
+                                   ("QKV", cfg.qkv_dim, BF16), ("Q", cfg.n_heads * Hd, BF16),
+                                   ("O", cfg.n_heads * Hd, BF16), ("T", E, BF16), ("G", cfg.hidden_dim, BF16),
+                                   ("U", cfg.hidden_dim, BF16)):
+                b[name] = torch.zeros((cap, cols) if cols else (cap,), dtype=dt, device=dev)
+            self._prefill_bufs = b
+        return {k: (v if k == "cap" else v[:S]) for k, v in b.items()}
 
     def prefill(self, token_ids, use_graph: bool = False) -> None:
         """Process the prompt at positions pos..pos+S-1; leaves logits of the last
@@ -433,8 +446,10 @@ class LlamaHIP:
         With ``use_graph`` the launches run as a hipGraph captured once per
         (prompt length, start position) -- after one eager run of that shape --
         and replayed afterwards, so the host issues one graph instead of ~150
-        kernels. Results are bit-identical to the eager path. Graphs are dropped
-        when the split-K workspace they point into is reallocated."""
+        kernels. Results are bit-identical to the eager path. At most
+        MAX_PREFILL_GRAPHS shapes are kept (least recently used dropped first);
+        all are dropped when the split-K workspace or the activation buffers
+        they point into are reallocated."""
         cfg = self.cfg
         ids = torch.as_tensor(token_ids, dtype=torch.int32).reshape(-1)
         S = int(ids.numel())
@@ -444,14 +459,17 @@ class LlamaHIP:
         b = self._pbufs(S)
         b["ids"].copy_(ids)
         key = (S, pos0)
-        graph = self._prefill_graphs.get(key) if use_graph else None
+        graph = self._prefill_graphs.pop(key, None) if use_graph else None
         if graph is not None:
+            self._prefill_graphs[key] = graph  # most recently used last
             graph.replay()
         else:
-            self._prefill_launches(S, pos0)  # also sizes the workspace the capture will use
+            self._prefill_launches(S, pos0)  # also sizes the workspace and buffers the capture will use
             if use_graph:
-                while self._prefill_graphs and len(self._prefill_graphs) >= self.MAX_PREFILL_GRAPHS:
-                    self._prefill_graphs.pop(next(iter(self._prefill_graphs)))  # the oldest shape first
+                if len(self._prefill_graphs) >= self.MAX_PREFILL_GRAPHS:
+                    torch.cuda.synchronize(self.device)  # a replay of the graph dropped below may still run
+                    while len(self._prefill_graphs) >= self.MAX_PREFILL_GRAPHS:
+                        self._prefill_graphs.pop(next(iter(self._prefill_graphs)))  # least recently used
                 self._prefill_graphs[key] = capture_graph(lambda: self._prefill_launches(S, pos0), self.device)
         self.pos.copy_(torch.tensor([pos0 + S - 1], dtype=torch.int32))
         self.host_pos = pos0 + S

@@ -1,0 +1,88 @@
+// Measurement probes for the launch and read floors that bound the short
+// decode kernels: an empty kernel (what one launch, or one node of a replayed
+// hipGraph, costs with no work) and a pure streaming read of n bytes (what
+// the memory system delivers to one launch of that size, with no arithmetic
+// and no stores beyond one word per workgroup). bench.py --mode floor times
+// both under the same graph protocol as the kernels they bound.
+#include "iron_common.hpp"
+#include "../../include/iron_hip.h"
+
+namespace iron {
+namespace {
+
+constexpr int kProbeThreads = 256;
+
+__global__ __launch_bounds__(kProbeThreads) void empty_kernel(int) {}
+
+// Workgroup b reads 16-byte chunks b * U * 256 + u * 256 + tid (u < U), every
+// load issued before the first use, and stores the XOR of its data to
+// sink[b] so that the loads are live. Chunks past the end re-read the last
+// chunk (an unconditional clamped load) and are dropped by a select.
+template <int U>
+__global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const uint4* __restrict__ src, long long n16,
+                                                                      uint32_t* __restrict__ sink) {
+  const long long base = static_cast<long long>(blockIdx.x) * U * kProbeThreads + threadIdx.x;
+  uint4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = ld_stream16(src + min(base + u * kProbeThreads, n16 - 1));
+  uint32_t acc = 0;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t w = v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    acc ^= (base + u * kProbeThreads < n16) ? w : 0u;
+  }
+  // fold the workgroup's words into one (wave shuffles, then the 4 waves through LDS)
+  __shared__ uint32_t red[kProbeThreads / kWave];
+  for (int off = 32; off > 0; off >>= 1) acc ^= __shfl_xor(acc, off, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kProbeThreads / kWave; ++w) t ^= red[w];
+    sink[blockIdx.x] = t;
+  }
+}
+
+}  // namespace
+}  // namespace iron
+
+using namespace iron;
+
+extern "C" int iron_probe_empty(int workgroups, void* stream) {
+  IRON_REQUIRE(workgroups > 0 && workgroups <= (1 << 20), "iron_probe_empty: workgroups=%d outside [1, 2^20]",
+               workgroups);
+  IRON_LAUNCH(empty_kernel, dim3(workgroups), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream), 0);
+  return check_launch("probe_empty");
+}
+
+extern "C" long long iron_probe_read_workgroups(long long nbytes, int loads_per_lane) {
+  if (nbytes <= 0 || nbytes % 16 || !(loads_per_lane == 1 || loads_per_lane == 2 || loads_per_lane == 4 ||
+                                      loads_per_lane == 8))
+    return -1;
+  const long long per_wg = static_cast<long long>(loads_per_lane) * kProbeThreads;
+  return (nbytes / 16 + per_wg - 1) / per_wg;
+}
+
+extern "C" int iron_probe_read(const void* src, long long nbytes, void* sink, long long sink_words,
+                               int loads_per_lane, void* stream) {
+  IRON_REQUIRE(src && sink, "iron_probe_read: null pointer");
+  IRON_REQUIRE(aligned16(src), "iron_probe_read: src must be 16-byte aligned");
+  const long long wgs = iron_probe_read_workgroups(nbytes, loads_per_lane);
+  IRON_REQUIRE(wgs > 0, "iron_probe_read: nbytes=%lld must be a positive multiple of 16 and loads_per_lane=%d one "
+               "of 1, 2, 4, 8", nbytes, loads_per_lane);
+  IRON_REQUIRE(wgs < (1LL << 31), "iron_probe_read: nbytes=%lld too large", nbytes);
+  IRON_REQUIRE(sink_words >= wgs, "iron_probe_read: sink holds %lld words, %lld needed", sink_words, wgs);
+  const uint4* s4 = static_cast<const uint4*>(src);
+  uint32_t* out = static_cast<uint32_t*>(sink);
+  const long long n16 = nbytes / 16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(wgs)), block(kProbeThreads);
+  switch (loads_per_lane) {
+    case 1: IRON_LAUNCH(stream_read_kernel<1>, grid, block, 0, s, s4, n16, out); break;
+    case 2: IRON_LAUNCH(stream_read_kernel<2>, grid, block, 0, s, s4, n16, out); break;
+    case 4: IRON_LAUNCH(stream_read_kernel<4>, grid, block, 0, s, s4, n16, out); break;
+    default: IRON_LAUNCH(stream_read_kernel<8>, grid, block, 0, s, s4, n16, out); break;
+  }
+  return check_launch("probe_read");
+}

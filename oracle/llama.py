@@ -94,8 +94,12 @@ class LlamaCPU:
         self.kc = [torch.empty(1, sh.n_kv_groups, 0, sh.head_dim) for _ in range(sh.n_layers)]
         self.vc = [torch.empty(1, sh.n_kv_groups, 0, sh.head_dim) for _ in range(sh.n_layers)]
 
-    def forward(self, token_ids: torch.Tensor) -> torch.Tensor:
-        """llama_cpu.py:221-285: logits (1, S, vocab) for token_ids (1, S)."""
+    def forward(self, token_ids: torch.Tensor, last_only: bool = False) -> torch.Tensor:
+        """llama_cpu.py:221-285: logits (1, S, vocab) for token_ids (1, S).
+
+        ``last_only`` applies the final norm and the head to the last position
+        only, (1, 1, vocab): the rows the accuracy gate reads, without the
+        S x vocab head product of a long prompt."""
         sh, w = self.shape, self.w
         x = torch.nn.functional.embedding(token_ids, w["model.embed_tokens.weight"])
         for i in range(sh.n_layers):
@@ -110,6 +114,8 @@ class LlamaCPU:
             h = rms_norm_forward(x, w[p + "post_attention_layernorm.weight"])
             x = x + swiglu_ffn_forward(h, w[p + "mlp.gate_proj.weight"], w[p + "mlp.up_proj.weight"],
                                        w[p + "mlp.down_proj.weight"])
+        if last_only:
+            x = x[:, -1:]
         x = rms_norm_forward(x, w["model.norm.weight"])
         head = w.get("lm_head.weight", w["model.embed_tokens.weight"])  # tied unless given (HF convention)
         return torch.nn.functional.linear(x, head)

@@ -94,3 +94,4 @@ def test_operator_catalog_resolves():
         assert hasattr(obj, "get_arg_spec") and hasattr(obj, "get_callable"), name
     with pytest.raises(AttributeError):
         getattr(catalog, "NoSuchOperator")
+

@@ -1,0 +1,62 @@
+"""GPU: the application entry point, run as a program and judged by the lines
+it prints, as iron/applications/llama_3.2_1b/test.py:44-113 runs llama_npu.py:
+the [Accuracy] lines against the fp32 CPU oracle (registered by
+tests/llama_app.py) with the reference's gates, the [Determinism] line, and the
+[Prefill]/[Decode] statistics the reference's metrics scrape. Full
+Llama-3.2-1B shape, random init, int4-g32 linears."""
+
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+ROOT = Path(__file__).resolve().parent.parent
+
+MAX_PREFILL_KL = 0.1  # iron/applications/llama_3.2_1b/test.py:80-81
+MAX_DECODE_KL = 0.05
+
+
+def _run(args, timeout=900):
+    res = subprocess.run([sys.executable, *args], cwd=ROOT, capture_output=True, text=True, timeout=timeout)
+    print(res.stdout[-3000:])
+    print(res.stderr[-3000:])
+    assert res.returncode == 0, f"exit {res.returncode}: {res.stderr[-2000:]}"
+    return res
+
+
+def test_app_check_accuracy(gpu):
+    res = _run(["tests/llama_app.py", "--prompt-len", "512", "--num-tokens", "16", "--check-accuracy"])
+    prefill_kl = float(re.search(r"\[Accuracy\] Prefill KL:\s*(\S+)", res.stdout).group(1))
+    decode_kl = float(re.search(r"\[Accuracy\] Decode max KL:\s*(\S+)", res.stdout).group(1))
+    mism = int(re.search(r"\[Accuracy\] Top-1 mismatches:\s*(\d+)", res.stdout).group(1))
+    # the reference gates the KL values only (test.py:93-95); mismatches are a reported metric
+    assert prefill_kl <= MAX_PREFILL_KL, prefill_kl
+    assert decode_kl <= MAX_DECODE_KL, decode_kl
+    assert 0 <= mism <= 17, mism
+
+
+def test_app_check_determinism(gpu):
+    res = _run(["-m", "iron_amd.applications.llama_3_2_1b", "--prompt-len", "128", "--num-tokens", "4",
+                "--check-determinism", "3"])
+    m = re.search(r"\[Determinism\] Differing runs:\s*(\d+)/(\d+)", res.stdout)
+    assert m and int(m.group(1)) == 0 and int(m.group(2)) == 4, m and m.group(0)
+
+
+def test_app_generate_statistics(gpu):
+    res = _run(["-m", "iron_amd.applications.llama_3_2_1b", "--prompt-len", "64", "--num-tokens", "8"])
+    ttft = float(re.search(r"\[Prefill\]\s*Time to first token:\s*([\d\.e\+-]+) s", res.stderr).group(1))
+    tps = float(re.search(r"\[Decode\]\s*Tokens per second:\s*([\d\.e\+-]+)", res.stderr).group(1))
+    assert ttft > 0 and tps > 0
+    assert len(re.findall(r"\[\d+\]", res.stdout)) == 8  # the generated token ids
+
+
+def test_app_accuracy_needs_a_reference(gpu):
+    """Without a registered CPU reference model, --check-accuracy refuses (the
+    library ships no CPU model)."""
+    res = subprocess.run([sys.executable, "-m", "iron_amd.applications.llama_3_2_1b", "--prompt-len", "16",
+                          "--num-tokens", "2", "--check-accuracy"], cwd=ROOT, capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 2 and "set_model_reference" in res.stderr

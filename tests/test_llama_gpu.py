@@ -223,3 +223,62 @@ def test_prefill_graph_matches_eager(gpu):
     gm.reset()
     gm.prefill(p1[:9], use_graph=True)
     assert list(gm._prefill_graphs) == [(5, 64), (9, 0)]
+
+
+def test_prefill_graph_reuse_eviction_and_regrowth(gpu):
+    """Captured prefill graphs under reuse and churn, each result bit-identical
+    to an eager model: a replay with other token ids of the same length; a
+    larger prompt issued right after a replay, without a host synchronisation
+    (its buffers and workspace grow, so every graph is dropped while the replay
+    may still run); least-recently-used eviction; and an evicted shape captured
+    again."""
+    from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
+
+    cfg = LlamaConfig(**MID)
+    w = random_weights(cfg, gpu, seed=8)
+    gm, em = LlamaHIP(cfg, w, device=gpu), LlamaHIP(cfg, w, device=gpu)
+    g = torch.Generator().manual_seed(9)
+
+    def ids(n):
+        return torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist()
+
+    def run(prompt):
+        for m in (gm, em):
+            m.reset()
+        gm.prefill(prompt, use_graph=True)
+        em.prefill(prompt)
+
+    def same():
+        torch.cuda.synchronize()
+        assert torch.equal(gm.logits, em.logits)
+        for i in range(cfg.n_layers):
+            assert torch.equal(gm.k_cache[i], em.k_cache[i]) and torch.equal(gm.v_cache[i], em.v_cache[i])
+
+    run(ids(40))  # capture (40, 0)
+    same()
+    run(ids(40))  # replay with other ids
+    same()
+    gm.reset()
+    gm.prefill(ids(40), use_graph=True)  # replay, then at once a longer prompt: no synchronize in between
+    big = ids(200)
+    gm.reset()
+    gm.prefill(big, use_graph=True)
+    em.reset()
+    em.prefill(big)
+    same()
+    assert list(gm._prefill_graphs) == [(200, 0)]
+    gm.MAX_PREFILL_GRAPHS = 2
+    a, b, c = ids(30), ids(31), ids(32)
+    run(a)
+    run(b)
+    run(a)  # hit: (30, 0) becomes the most recently used
+    run(c)  # evicts (31, 0), the least recently used
+    assert list(gm._prefill_graphs) == [(30, 0), (32, 0)]
+    same()
+    run(ids(31))  # the evicted shape, captured again
+    same()
+    run(ids(31))  # and replayed
+    same()
+    assert list(gm._prefill_graphs) == [(32, 0), (31, 0)]
+    # buffers stay sized by the longest prompt (256 rows for 200 tokens)
+    assert gm._prefill_bufs["cap"] == 256

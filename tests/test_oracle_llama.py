@@ -61,3 +61,18 @@ def test_product_rope_table_matches_oracle():
     a = compute_rope_angles(64, 4096, 500000.0, ops.LLAMA3_FREQ_CONFIG)
     b = ops.rope_angles_table(64, 4096)
     assert torch.allclose(a, b, atol=1e-5, rtol=0)
+
+
+def test_oracle_last_only_matches_full_forward():
+    """forward(last_only=True) is the last row of the full forward, also after a
+    cached prefix."""
+    shape = llama.LlamaShape(vocab_size=300, emb_dim=128, n_layers=2, n_heads=2, n_kv_groups=1, hidden_dim=256)
+    w = _tiny_weights(shape, seed=3)
+    angles = ops.rope_angles_table(64, 64)
+    a, b = llama.LlamaCPU(shape, w, angles), llama.LlamaCPU(shape, w, angles)
+    for ids in (torch.tensor([[5, 17, 3, 250, 99]]), torch.tensor([[8, 1, 2]])):
+        full = a.forward(ids)
+        last = b.forward(ids, last_only=True)
+        assert last.shape == (1, 1, 300)
+        # a one-row product may sum in another order than the full one: fp32 rounding only
+        assert torch.allclose(last[0, 0], full[0, -1], atol=1e-5, rtol=1e-5)
