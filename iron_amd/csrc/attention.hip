@@ -1,13 +1,16 @@
-// GQA attention for decode (split-K flash-decode) and causal prefill.
+// GQA attention for decode (split-K flash-decode in one kernel) and causal prefill.
 //
 // Decode: one new token. A workgroup owns (KV head j, a chunk of 64 cache
 // positions) and serves the G = H/Hkv query heads that share KV head j, so
 // every K/V byte is read from HBM once for all of them. Inside the chunk the
 // softmax is exact in fp32 (scores scaled by log2(e)/sqrt(D), exp2); the
 // chunk's unnormalised output, maximum and sum go to a workspace, and a second
-// small kernel merges the chunks. (Merging in the last-arriving workgroup
-// would need an agent-scope fence per workgroup, which on this GPU writes back
-// and invalidates the whole per-XCD L2: far dearer than one more launch.)
+// small kernel merges the chunks. (Merging in the last-arriving workgroup was
+// measured slower: cross-XCD visibility of the partials needs either an
+// agent-scope release, which writes back the whole per-XCD L2 and serialises
+// across workgroups, or write-through stores plus an arrival atomic per
+// workgroup, whose round trips and same-address serialisation cost more than
+// the second launch.)
 // RoPE for q and the new k is applied on load (two-halves rotation, row `pos`
 // of an fp32 [cos, sin] interleaved table, result rounded to bf16 as the RoPE
 // operator does), and the new k/v are written into the caches at `pos` by the
@@ -18,11 +21,12 @@
 #include "iron_common.hpp"
 #include "../../include/iron_hip.h"
 
+#include <type_traits>
+
 namespace iron {
 namespace {
 
-constexpr int kDecChunk = 64;  // cache positions per workgroup
-constexpr int kDecRows = kDecChunk / 32;  // cache rows per thread (32 row slots x 8 dim chunks)
+constexpr int kDecChunk = 64;  // cache positions per workgroup (4 waves x 16)
 constexpr int kDecThreads = 256;
 constexpr int kD = 64;         // head dim (the reference MHA supports d = 64 only)
 
@@ -74,55 +78,83 @@ __device__ __forceinline__ void rope_chunk(const uint4 own, const uint4 pair, co
   }
 }
 
-// Partials of one chunk (kDecChunk positions) of KV head j for its G query
-// heads. Measured at Llama's shape: 64 positions beat 32 (-1% decode at short
-// context, 4% slower config 3) and 128 (2% slower decode at KV 4096, 11%
-// slower config 3).
-// Thread -> (position rows r, r + 32, ... of the chunk, dims 8c..8c+7). Every
-// global load the workgroup needs (K/V rows, q and its RoPE partner, the
-// table row, the new k/v) is issued right after `pos` is known, before any
-// barrier, so the kernel pays one memory round trip after the position. q is
-// rotated once per workgroup (one element per thread) and shared through LDS;
-// a per-thread rotation of its own chunks would repeat the work 32 times.
+// Lanes l and l ^ 32 of a and b summed in one exchange (v_permlane32_swap_b32
+// swaps the upper 32 lanes of its first operand with the lower 32 of its
+// second): lanes 0..31 return a[l] + a[l ^ 32], lanes 32..63 b[l] + b[l ^ 32].
+// Inline assembly: this compiler's builtins for the permlane swaps return the
+// first result in place of the second (seen in the generated code). The s_nop
+// covers the VALU-write to permlane-read hazard.
+__device__ __forceinline__ float fold32(float a, float b) {
+  unsigned x = __builtin_bit_cast(unsigned, a), y = __builtin_bit_cast(unsigned, b);
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
+
+// The same over lanes l and l ^ 16 (v_permlane16_swap_b32 swaps the odd
+// 16-lane rows of its first operand with the even rows of its second): rows 0
+// and 2 return a[l] + a[l ^ 16], rows 1 and 3 b[l] + b[l ^ 16].
+__device__ __forceinline__ float fold16(float a, float b) {
+  unsigned x = __builtin_bit_cast(unsigned, a), y = __builtin_bit_cast(unsigned, b);
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+}
+
+// 2^x by v_exp_f32 alone, for x <= 0 (softmax weights): results below 2^-126
+// flush to zero, which the weights tolerate; elsewhere exp2f's value.
+__device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// One decode step of KV head j (blockIdx.y) for its G query heads; workgroup
+// s (blockIdx.x) owns cache positions [64 s, 64 s + 64).
+//
+// Wave w of the workgroup takes positions 64 s + 16 w + [0, 16): lane
+// (r = lane / 8, c = lane % 8) holds rows r and r + 8 of them, dims 8c..8c+7.
+// Every global load (K/V rows, q and the table row, the owner's new k/v) is
+// issued as soon as `pos` is known. q is rotated once per workgroup (one
+// element per thread) into LDS as bf16. Scores are bf16 dot products
+// (v_dot2_f32_bf16: exact products, fp32 sums) summed over the 8 lanes of a
+// row by DPP; the softmax statistics of the wave's 16 rows come from wave-wide
+// DPP reductions, and the wave's unnormalised output (G x 64 values, 8G per
+// lane) is summed over the 8 rows of lanes with two permlane folds and one
+// DPP step, which leave each lane 2G totals. The four waves meet once in LDS
+// to form the chunk's partial (output, maximum, sum), written to the
+// workspace for gqa_combine_kernel.
 template <int G>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int NW = kDecThreads / kWave;
   constexpr int PS = part_stride<G>();
-  __shared__ __attribute__((aligned(16))) float q_s[G][D];  // rotated q
-  __shared__ float max_s[NW][G];
-  __shared__ float sum_s[NW][G];
-  // per (head, position row, dim); rows padded to 65 floats so the 8x8 (row, chunk) lanes of a
-  // wave writing one dim spread over the banks (a 64-float row would put 16 lanes on one bank)
-  __shared__ float o_s[G][kDecThreads / 8][D + 1];
+  constexpr int NV = 8 * G;  // unnormalised output values per lane before the folds
+  __shared__ __attribute__((aligned(16))) uint16_t q_s[G * D];  // rotated q, bf16
+  __shared__ float wm_s[NW][G], wl_s[NW][G];
+  __shared__ __attribute__((aligned(16))) float wo_s[NW][G * D];
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
   const int s = blockIdx.x, j = blockIdx.y;
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * kDecChunk;
   if (p0 >= L) return;
-  const int c = tid & 7, r = tid >> 3;
+  const int c = lane & 7, r = lane >> 3;
   const bool lower = c < 4;
-  const bool owner = pos >= p0 && pos < p0 + kDecChunk;
+  const int wrow0 = p0 + 16 * w;
+  const bool owner = pos >= wrow0 && pos < wrow0 + 16;
 
-  // Cache rows of the chunk: unconditional loads of a clamped row (a guarded
-  // load compiled to a branch waiting for its data); rows >= pos are replaced
-  // below (the new token) or masked (past it).
-  uint4 kraw[kDecRows], vraw[kDecRows];
+  // cache rows: unconditional loads of a clamped row (a guarded load compiled
+  // to a branch that waited for its data); rows >= pos are replaced below
+  // (the new token) or masked (past it)
+  uint4 kraw[2], vraw[2];
 #pragma unroll
-  for (int h = 0; h < kDecRows; ++h) {
-    const int p = min(p0 + r + 32 * h, a.max_len - 1);
+  for (int h = 0; h < 2; ++h) {
+    const int p = min(wrow0 + r + 8 * h, a.max_len - 1);
     const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
     kraw[h] = ld_stream16(a.k_cache + off);
     vraw[h] = ld_stream16(a.v_cache + off);
   }
   const float* angrow = a.angles + static_cast<size_t>(pos) * D;
-  // the owner's table row and new k/v, in flight with the cache rows
   float ang[16];
   uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
-  if (owner) {
+  if (owner) {  // the new token's table entries and k/v, in flight with the cache rows
     const float4* ap = reinterpret_cast<const float4*>(angrow + (c & 3) * 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -136,118 +168,129 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (c ^ 4) * 8);
     vn = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + c * 8);
   }
-  // q rotated once per workgroup: thread t -> element (t / 64, t % 64) into LDS
   const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
   for (int t = tid; t < G * D; t += kDecThreads) {
     const int d = t % D, i = d & 31;
     const float x = bf16_to_f32(qh[t]), xp = bf16_to_f32(qh[t ^ 32]);
     const float cs = angrow[2 * i], sn = angrow[2 * i + 1];
-    q_s[t / D][d] = bf16_to_f32(f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn));
+    q_s[t] = f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn);
   }
   __syncthreads();
-  float qv[G][8];
+  uint4 qk[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float4 lo = *reinterpret_cast<const float4*>(&q_s[g][c * 8]);
-    const float4 hi = *reinterpret_cast<const float4*>(&q_s[g][c * 8 + 4]);
-    qv[g][0] = lo.x; qv[g][1] = lo.y; qv[g][2] = lo.z; qv[g][3] = lo.w;
-    qv[g][4] = hi.x; qv[g][5] = hi.y; qv[g][6] = hi.z; qv[g][7] = hi.w;
-  }
-  float kf[kDecRows][8], vf[kDecRows][8];
-  bool valid[kDecRows];
+  for (int g = 0; g < G; ++g) qk[g] = *reinterpret_cast<const uint4*>(&q_s[g * D + c * 8]);
+
+  // One code path for waves whose 16 rows are all valid and none is the new
+  // token (every wave but the last one or two), one with the masks and the
+  // owner's append.
+  const bool full = wrow0 + 16 <= L && !owner;  // wave-uniform
+  auto wave_body = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    // K rows as packed bf16, V rows as floats (zero past pos: 0 * stale data must not reach o)
+    uint32_t kw[2][4];
+    float vf[2][8];
+    bool valid[2];
 #pragma unroll
-  for (int h = 0; h < kDecRows; ++h) {
-    const int p = p0 + r + 32 * h;
-    valid[h] = p < L;
-    if (p == pos) {  // the new token: rotate k, append k/v to the caches
-      rope_chunk(kna, knb, ang, lower, kf[h]);
-      unpack8(vn, vf[h]);
-      uint32_t kw[4];
+    for (int h = 0; h < 2; ++h) {
+      const int p = wrow0 + r + 8 * h;
+      valid[h] = FULL || p < L;
+      if (!FULL && p == pos) {  // the new token: rotate k, append k/v to the caches
+        float kr[8];
+        rope_chunk(kna, knb, ang, lower, kr);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) kw[e] = pack_bf16x2(kf[h][2 * e], kf[h][2 * e + 1]);  // exact: already bf16 values
-      const size_t off = (static_cast<size_t>(j) * a.max_len + pos) * D + c * 8;
-      *reinterpret_cast<uint4*>(a.k_cache + off) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-      *reinterpret_cast<uint4*>(a.v_cache + off) = vn;
-    } else {
-      unpack8(kraw[h], kf[h]);
-      unpack8(vraw[h], vf[h]);
+        for (int e = 0; e < 4; ++e) kw[h][e] = pack_bf16x2(kr[2 * e], kr[2 * e + 1]);  // exact: bf16 values
+        unpack8(vn, vf[h]);
+        const size_t off = (static_cast<size_t>(j) * a.max_len + pos) * D + c * 8;
+        *reinterpret_cast<uint4*>(a.k_cache + off) = make_uint4(kw[h][0], kw[h][1], kw[h][2], kw[h][3]);
+        *reinterpret_cast<uint4*>(a.v_cache + off) = vn;
+      } else {
+        kw[h][0] = kraw[h].x;
+        kw[h][1] = kraw[h].y;
+        kw[h][2] = kraw[h].z;
+        kw[h][3] = kraw[h].w;
+        unpack8(vraw[h], vf[h]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {  // rows past pos hold stale cache data: 0 * NaN must not reach o
-        kf[h][e] = valid[h] ? kf[h][e] : 0.f;
-        vf[h][e] = valid[h] ? vf[h][e] : 0.f;
+        for (int e = 0; e < 8; ++e) vf[h][e] = FULL || valid[h] ? vf[h][e] : 0.f;
       }
     }
-  }
 
-  // scores in the log2 domain; the 8 lanes of a position sum their partial dots
-  float sc[kDecRows][G];
+    // scores in the log2 domain; the 8 lanes of a row sum their partial dots
+    float sc[2][G];
 #pragma unroll
-  for (int h = 0; h < kDecRows; ++h)
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = dot2_bf16(qk[g].x, kw[h][0], 0.f);
+        d = dot2_bf16(qk[g].y, kw[h][1], d);
+        d = dot2_bf16(qk[g].z, kw[h][2], d);
+        d = dot2_bf16(qk[g].w, kw[h][3], d);
+        d = add_dpp<0xB1>(d);   // + lane ^ 1
+        d = add_dpp<0x4E>(d);   // + lane ^ 2
+        d = add_dpp<0x141>(d);  // + lane 7-i of the 8: full 8-lane sum
+        sc[h][g] = FULL || valid[h] ? d * a.scale_log2 : -INFINITY;
+      }
+
+    // the wave's statistics and unnormalised output over its 16 rows
+    float ov[NV];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float d = 0.f;
+      const float m = wave_max(fmaxf(sc[0][g], sc[1][g]));  // -inf only when all 16 rows are past pos
+      const float e0 = FULL || valid[0] ? exp2_weight(sc[0][g] - m) : 0.f;
+      const float e1 = FULL || valid[1] ? exp2_weight(sc[1][g] - m) : 0.f;
+      const float l = wave_sum(c == 0 ? e0 + e1 : 0.f);
+      if (lane == 0) {
+        wm_s[w][g] = m;
+        wl_s[w][g] = l;
+      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[h][e], d);
-      d = add_dpp<0xB1>(d);   // + lane ^ 1
-      d = add_dpp<0x4E>(d);   // + lane ^ 2
-      d = add_dpp<0x141>(d);  // + lane 7-i of the 8: full 8-lane sum
-      sc[h][g] = valid[h] ? d * a.scale_log2 : -INFINITY;
+      for (int e = 0; e < 8; ++e) ov[g * 8 + e] = fmaf(e0, vf[0][e], e1 * vf[1][e]);
     }
-
-  // chunk maximum per head (finite: position p0 < L is always valid)
+    // sum over the 8 rows r (lane bits 3..5): value k pairs with k + NV/2 across
+    // lane bit 5, then with k + NV/4 across bit 4, then a DPP step over bit 3
+    float o2[NV / 2], o4[NV / 4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = sc[0][g];
+    for (int k = 0; k < NV / 2; ++k) o2[k] = fold32(ov[k], ov[k + NV / 2]);
 #pragma unroll
-    for (int h = 1; h < kDecRows; ++h) m = fmaxf(m, sc[h][g]);
-    m = wave_max(m);
-    if (lane == 0) max_s[wave][g] = m;
-  }
+    for (int k = 0; k < NV / 4; ++k) {
+      const float t = fold16(o2[k], o2[k + NV / 4]);
+      o4[k] = t + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x128, 0xf,
+                                                                            0xf, false));  // row_ror:8 = lane ^ 8
+    }
+    // lane holds totals k = (lane bit 5) NV/2 + (lane bit 4) NV/4 + [0, NV/4): value k is (g = k / 8, dim 8c + k % 8)
+    if (((lane >> 3) & 1) == 0) {
+      const int k0 = (lane >> 5) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+#pragma unroll
+      for (int k = 0; k < NV / 4; ++k) {
+        const int kk = k0 + k;
+        wo_s[w][(kk / 8) * D + c * 8 + kk % 8] = o4[k];
+      }
+    }
+  };
+  if (full)
+    wave_body(std::true_type{});
+  else
+    wave_body(std::false_type{});
   __syncthreads();
-  float mloc[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = max_s[0][g];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) m = fmaxf(m, max_s[w][g]);
-    mloc[g] = m;
-  }
 
-  // probabilities, their sum (one lane per position counts), and this
-  // thread's share of the unnormalised output
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float ev[kDecRows], es = 0.f;
-#pragma unroll
-    for (int h = 0; h < kDecRows; ++h) {
-      ev[h] = valid[h] ? exp2f(sc[h][g] - mloc[g]) : 0.f;
-      es += ev[h];
-    }
-    const float l = wave_sum(c == 0 ? es : 0.f);
-    if (lane == 0) sum_s[wave][g] = l;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float o = 0.f;
-#pragma unroll
-      for (int h = 0; h < kDecRows; ++h) o = fmaf(ev[h], vf[h][e], o);
-      o_s[g][r][c * 8 + e] = o;
-    }
-  }
-  __syncthreads();
+  // the chunk's partial: the four waves merged
   float* part = a.part + (static_cast<size_t>(j) * a.nsplit + s) * PS;
   for (int t = tid; t < G * D; t += kDecThreads) {
-    const int g = t / D, d = t % D;
-    float acc = 0.f;
-#pragma unroll 8
-    for (int rr = 0; rr < kDecThreads / 8; ++rr) acc += o_s[g][rr][d];
-    part[t] = acc;
-  }
-  if (tid < G) {
-    float l = 0.f;
+    const int g = t / D;
+    float M = wm_s[0][g];  // finite: position p0 < L is in wave 0
 #pragma unroll
-    for (int w = 0; w < NW; ++w) l += sum_s[w][tid];
-    part[G * D + tid] = mloc[tid];
-    part[G * D + G + tid] = l;
+    for (int ww = 1; ww < NW; ++ww) M = fmaxf(M, wm_s[ww][g]);
+    float o = 0.f, l = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float f = exp2_weight(wm_s[ww][g] - M);  // 0 for a wave whose rows are all past pos
+      o = fmaf(f, wo_s[ww][t], o);
+      l = fmaf(f, wl_s[ww][g], l);
+    }
+    part[t] = o;
+    if (t % D == 0) {
+      part[G * D + g] = M;
+      part[G * D + G + g] = l;
+    }
   }
 }
 
@@ -334,6 +377,53 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
     }
     a.out[static_cast<size_t>(h) * D + d] = f32_to_bf16(ot / lt);
   }
+}
+
+// Merge of the chunk partials with one wave per query head (Hkv * G
+// workgroups of 64 threads): lane i holds the statistics (maximum, sum) of
+// chunks i, i + 64, ..., lane d accumulates output dim d, and each chunk's
+// weight reaches every lane by readlane. The loads of the first 64 chunks are
+// issued before the position is read, so a context of up to 4096 positions
+// costs one memory round trip. Chunks past the active count are dropped by
+// selects (their workspace may hold anything).
+template <int G>
+__global__ __launch_bounds__(kWave) void gqa_merge_kernel(DecodeArgs a) {
+  constexpr int D = kD;
+  constexpr int PS = part_stride<G>();
+  const int lane = threadIdx.x;
+  const int h = blockIdx.x, j = h / G, g = h % G;
+  const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
+  const float* pl = base + static_cast<size_t>(min(lane, a.nsplit - 1)) * PS;
+  float mb = pl[G * D + g], lb = pl[G * D + G + g];
+  float ob[kWave];
+#pragma unroll
+  for (int u = 0; u < kWave; ++u) ob[u] = base[static_cast<size_t>(min(u, a.nsplit - 1)) * PS + g * D + lane];
+  const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+  if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
+  const int nact = (pos + kDecChunk) / kDecChunk;
+  float M = lane < nact ? mb : -INFINITY;
+  for (int i = lane + kWave; i < nact; i += kWave) M = fmaxf(M, base[static_cast<size_t>(i) * PS + G * D + g]);
+  M = wave_max(M);  // finite: chunk 0 is active
+  float acc = 0.f, Ls = 0.f;
+  for (int b0 = 0; b0 < nact; b0 += kWave) {
+    if (b0 > 0) {  // contexts past 64 chunks: the next 64
+      const float* pb = base + static_cast<size_t>(min(b0 + lane, nact - 1)) * PS;
+      mb = pb[G * D + g];
+      lb = pb[G * D + G + g];
+#pragma unroll
+      for (int u = 0; u < kWave; ++u) ob[u] = base[static_cast<size_t>(min(b0 + u, nact - 1)) * PS + g * D + lane];
+    }
+    const bool live = b0 + lane < nact;
+    const float wgt = live ? exp2f(mb - M) : 0.f;
+    Ls = fmaf(wgt, live ? lb : 0.f, Ls);
+#pragma unroll
+    for (int u = 0; u < kWave; ++u) {
+      const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+      acc = fmaf(wu, b0 + u < nact ? ob[u] : 0.f, acc);
+    }
+  }
+  Ls = wave_sum(Ls);
+  a.out[static_cast<size_t>(h) * D + lane] = f32_to_bf16(acc / Ls);
 }
 
 // ---------------------------------------------------------------------------
@@ -705,26 +795,26 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
   return 256 + part;  // 256 reserved bytes, then partials
 }
 
-extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
-                               const float* angles, int angle_rows, void* out, void* workspace, int n_heads,
-                               int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
-                               void* stream) {
-  IRON_REQUIRE(q && k_new && v_new && k_cache && v_cache && angles && out && workspace,
-               "iron_gqa_decode: null pointer");
-  IRON_REQUIRE(head_dim == kD, "iron_gqa_decode: head_dim=%d (only 64 is supported)", head_dim);
+// Checks and launches of one GQA decode step with its partials in `workspace`
+// (iron_gqa_decode_workspace_bytes() of the shape, 256-byte aligned).
+static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
+                             void* v_cache, const float* angles, int angle_rows, void* out, void* workspace,
+                             int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
+                             float scale, void* stream) {
+  IRON_REQUIRE(q && k_new && v_new && k_cache && v_cache && angles && out && workspace, "%s: null pointer", who);
+  IRON_REQUIRE(head_dim == kD, "%s: head_dim=%d (only 64 is supported)", who, head_dim);
   IRON_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
-               "iron_gqa_decode: n_heads=%d must be a multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+               "%s: n_heads=%d must be a multiple of n_kv_heads=%d", who, n_heads, n_kv_heads);
   const int G = n_heads / n_kv_heads;
-  IRON_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "iron_gqa_decode: group size %d not in {1,2,4,8}", G);
-  IRON_REQUIRE(n_kv_heads * 4 <= 256, "iron_gqa_decode: at most 64 KV heads");
-  IRON_REQUIRE(max_len > 0 && angle_rows > 0, "iron_gqa_decode: max_len and angle_rows must be positive");
+  IRON_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "%s: group size %d not in {1,2,4,8}", who, G);
+  IRON_REQUIRE(n_kv_heads * 4 <= 256, "%s: at most 64 KV heads", who);
+  IRON_REQUIRE(max_len > 0 && angle_rows > 0, "%s: max_len and angle_rows must be positive", who);
   IRON_REQUIRE(pos_dev || (pos >= 0 && pos < max_len && pos < angle_rows),
-               "iron_gqa_decode: pos=%d outside the cache (max_len=%d) or angle table (%d rows)", pos, max_len,
-               angle_rows);
+               "%s: pos=%d outside the cache (max_len=%d) or angle table (%d rows)", who, pos, max_len, angle_rows);
   IRON_REQUIRE(aligned16(q) && aligned16(k_new) && aligned16(v_new) && aligned16(k_cache) && aligned16(v_cache) &&
                    aligned16(angles),
-               "iron_gqa_decode: q, k_new, v_new, the caches and the angle table must be 16-byte aligned");
-  IRON_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "iron_gqa_decode: workspace must be 256-byte aligned");
+               "%s: q, k_new, v_new, the caches and the angle table must be 16-byte aligned", who);
+  IRON_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "%s: workspace must be 256-byte aligned", who);
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k_new = static_cast<const uint16_t*>(k_new);
@@ -761,7 +851,15 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
       IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, cblock, 0, s, a);
       break;
   }
-  return check_launch("gqa_decode");
+  return check_launch(who);
+}
+
+extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                               const float* angles, int angle_rows, void* out, void* workspace, int n_heads,
+                               int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
+                               void* stream) {
+  return gqa_decode_launch("iron_gqa_decode", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, workspace,
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream);
 }
 
 extern "C" int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads,
