@@ -8,7 +8,9 @@
  *  - `stream` is a hipStream_t (NULL = the legacy default stream). Calls are
  *    stream-ordered and asynchronous; nothing here synchronises the host.
  *  - The library never allocates device memory. Where a kernel needs scratch
- *    the caller passes a workspace sized by the matching *_workspace_bytes().
+ *    the caller passes a workspace sized by the matching *_workspace_bytes();
+ *    only iron_gqa_decode_noalloc uses a fixed array that the library's code
+ *    object holds per GPU instead.
  *  - Return value: 0 on success, IRON_EINVAL (22) for a rejected argument, or a
  *    hipError_t from the launch. iron_last_error() then describes the failure
  *    (thread-local, valid until the next failing call on that thread).
@@ -194,6 +196,23 @@ long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_
 int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                     const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
                     int head_dim, int max_len, int pos, const int* pos_dev, float scale, void* stream);
+
+/* iron_gqa_decode without a workspace argument: the partials go to a scratch
+ * array the library holds in device memory, one per GPU, for the life of the
+ * process (iron_gqa_decode_noalloc_max_bytes(), 4 MiB: at the Llama-3.2-1B
+ * shape, 32/8 heads, up to max_len 31744). It allocates nothing, so callers
+ * that cannot allocate device memory (code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc) can use it. Shapes whose
+ * iron_gqa_decode_workspace_bytes() exceed the maximum are rejected
+ * (IRON_EINVAL) before anything runs. Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race;
+ * stream-ordered calls are safe. The array needs no initialisation (every
+ * partial is written before it is read). Same results as iron_gqa_decode.
+ * No counterpart in the reference: it exists for the callers above. */
+long long iron_gqa_decode_noalloc_max_bytes(void);
+int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                            const float* angles, int angle_rows, void* out, int n_heads, int n_kv_heads, int head_dim,
+                            int max_len, int pos, const int* pos_dev, float scale, void* stream);
 
 /* Flash attention over strided Q (H,Sq,64), K/V (Hkv,Skv,64), out (H,Sq,64)
  * (element strides per head and per row; rows 16-byte aligned). Query row i

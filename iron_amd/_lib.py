@@ -40,6 +40,7 @@ SIGNATURES: dict[str, list] = {
     "iron_softmax": [_P, _P, _I, _I, _I, _P, _P],
     "iron_rope": [_P, _P, _I, _P, _I, _I, _I, _I, _P],
     "iron_gqa_decode": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P],
+    "iron_gqa_decode_noalloc": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _F, _P],
     "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
     "iron_gemm_bf16_nt": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _P],
     "iron_gemm_bf16_nt_splitk": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _I, _P, _LL, _P],
@@ -64,6 +65,7 @@ SIGNATURES: dict[str, list] = {
 # ... except these queries, which return a value.
 QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
+    "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
     "iron_probe_read_workgroups": (_LL, [_LL, _I]),

@@ -21,6 +21,7 @@
 #include "iron_common.hpp"
 #include "../../include/iron_hip.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace iron {
@@ -796,7 +797,9 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
 }
 
 // Checks and launches of one GQA decode step with its partials in `workspace`
-// (iron_gqa_decode_workspace_bytes() of the shape, 256-byte aligned).
+// (iron_gqa_decode_workspace_bytes() of the shape, 256-byte aligned); shared
+// by the entry point that takes a workspace and the one that uses the
+// library's own scratch array.
 static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
                              void* v_cache, const float* angles, int angle_rows, void* out, void* workspace,
                              int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
@@ -859,6 +862,63 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
                                int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
                                void* stream) {
   return gqa_decode_launch("iron_gqa_decode", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, workspace,
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream);
+}
+
+// The workspace of iron_gqa_decode_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends. Host code never passes `scratch`
+// itself to a kernel (on the host that name is a stand-in, not a device
+// address): its device address is looked up once per device with
+// hipGetSymbolAddress, with that device current, and only that address is used.
+static constexpr long long kDecodeScratchBytes = 4LL << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device), or nullptr with the error set.
+static void* decode_scratch_ptr(const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("%s: device %d beyond the %d devices the library tracks", who, dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("%s: hipGetSymbolAddress of the scratch array failed on device %d: %s", who, dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" long long iron_gqa_decode_noalloc_max_bytes(void) { return kDecodeScratchBytes; }
+
+extern "C" int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new, void* k_cache,
+                                       void* v_cache, const float* angles, int angle_rows, void* out, int n_heads,
+                                       int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
+                                       float scale, void* stream) {
+  const long long need = iron_gqa_decode_workspace_bytes(n_heads, n_kv_heads, head_dim, max_len);
+  IRON_REQUIRE(need > 0, "iron_gqa_decode_noalloc: invalid shape (n_heads=%d, n_kv_heads=%d, head_dim=%d, max_len=%d)",
+               n_heads, n_kv_heads, head_dim, max_len);
+  IRON_REQUIRE(need <= kDecodeScratchBytes,
+               "iron_gqa_decode_noalloc: this shape needs %lld bytes of scratch, more than the %lld the library "
+               "holds per device (use iron_gqa_decode with a workspace)", need, kDecodeScratchBytes);
+  void* ws = decode_scratch_ptr("iron_gqa_decode_noalloc");
+  if (!ws) return IRON_EINVAL;
+  return gqa_decode_launch("iron_gqa_decode_noalloc", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, ws,
                            n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream);
 }
 

@@ -95,3 +95,18 @@ def test_operator_catalog_resolves():
     with pytest.raises(AttributeError):
         getattr(catalog, "NoSuchOperator")
 
+
+def test_gqa_decode_noalloc_rejects_oversized_shape_on_host():
+    """The no-allocation decode attention refuses, before touching a GPU, a shape
+    whose partials exceed the library's scratch array."""
+    from iron_amd import _lib
+
+    cap = _lib.query("iron_gqa_decode_noalloc_max_bytes")
+    assert cap == 4 << 20
+    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 31744) <= cap
+    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 31745) > cap
+    with pytest.raises(_lib.IronHipError, match="more than the 4194304"):
+        _lib.call("iron_gqa_decode_noalloc", 16, 16, 16, 16, 16, 16, 32768, 16, 32, 8, 64, 32768, 0, None, 0.125,
+                  None)
+    with pytest.raises(_lib.IronHipError, match="invalid shape"):
+        _lib.call("iron_gqa_decode_noalloc", 16, 16, 16, 16, 16, 16, 128, 16, 32, 8, 32, 128, 0, None, 0.125, None)
