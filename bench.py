@@ -1,38 +1,58 @@
 #!/usr/bin/env python3
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--mode full|gemv|model|prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                    [--mode full|gemv|model|prefill|attention|floor]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
 runs only the Llama configuration; --mode prefill only the config 5 prefill
-GEMM and the 3968-token causal attention (for kernel traces and counters).
+GEMM and the 3968-token causal attention; --mode attention the GQA decode
+attention at config 3 and at KV 4096; --mode floor the per-launch floors (an
+empty kernel as a graph node, a pure streaming read of the decode kernels'
+sizes). The modes exist for kernel traces and counters.
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
-(9,457,664 B per step). A step is one launch over one weight copy; copies
-rotate through a pool of >= 512 MiB so the 256 MiB Infinity Cache cannot hold
-the working set. Inputs are resident in HBM before the timed region; the
-timed region is exactly K launches on one stream between two synchronizes,
-issued as replays of a hipGraph that holds a chunk of consecutive launches
-(<= 100, a divisor of K) -- the way the decode step issues its kernels -- so
-the host's per-launch cost (about 3 us in the HIP runtime plus the Python
-call) does not bound the rate. ``python_launch_us`` reports the same kernel
-launched one call at a time from Python.
+(9,457,664 B per step). A step is one launch over one weight copy. Inputs are
+resident in HBM before the timed region.
 
-``roofline``: algorithmic bytes / the kernel's mean device time per launch,
-which is the timed region (HIP events on the launch stream around the K
-back-to-back launches) divided by K.
+Cache-proof rotation (every GPU figure): copies of a kernel's working set fill
+a pool of >= 640 MiB, launch i reads copy i % copies, and a copy is read again
+only after every other copy has been (>= 640 MiB read since), so the 256 MiB
+Infinity Cache cannot serve a timed launch at any step count. Launches are
+issued from captured hipGraphs -- the way the decode step issues its kernels
+-- so the host's per-launch cost (about 3 us in the HIP runtime plus the
+Python call) does not bound the rate; ``python_launch_us`` reports the same
+kernel launched one call at a time from Python.
+
+Headline timing: one graph holds a lead of one launch per copy, then the K
+timed launches; its replay time minus the replay time of the lead alone is
+the device time of exactly the K launches (HIP events on the launch stream;
+each replay is queued behind an untimed replay of the lead, so the host's
+graph-launch latency stays out). The difference cancels the fixed cost a
+graph replay carries at its start and end, so the per-launch time does not
+depend on K. Other configs: a graph of a multiple of `copies` launches (>= a
+few hundred), replayed untimed then timed; per-launch time = timed replay / n,
+median of 5.
+
+``roofline``: algorithmic bytes / that per-launch device time. ``traffic``: HBM
+bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the
+counter's reading for a copy of known size.
 ``cpu_baseline``: the CPU oracle (torch: dequantise, then fp32 matvec) timed
 on the host cores on a bounded sample; ``cpu_baseline.model_decode`` times the
-oracle's fp32 Llama forward (greedy decode, Llama-3.2-1B shape) the same way,
-beside the GPU decode rate in ``extra.llama_cfg5``. ``extra`` carries the other BASELINE
-configurations: bf16 GEMV (cfg 1), GQA decode (cfg 3), SwiGLU block bf16 and
-int4 (cfg 4), the prefill GEMM and the Llama-3.2-1B-shaped model (cfg 5:
-prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096 window).
-Its ``ttft_ms`` replays the prefill graph captured beforehand for the prompt
-length (``ttft_eager_ms``: the same prefill issued kernel by kernel); the
-token ids are copied from the host inside both timings.
+oracle's fp32 Llama forward (greedy decode, Llama-3.2-1B shape) the same way.
+Each config in ``extra`` carries its own ``cpu_baseline`` (configs 1, 3, 4 and
+the config 5 prefill GEMM), in the GPU figure's unit, with the core count.
+``extra`` carries the other BASELINE configurations: bf16 GEMV (cfg 1), GQA
+decode (cfg 3, and at KV 4096), SwiGLU block bf16 and int4 (cfg 4), the
+prefill GEMM with cold weights and the Llama-3.2-1B-shaped model (cfg 5:
+prefill 512 tokens, 128 greedy decode steps; plus the KV 3968 -> 4096
+window). Its ``ttft_ms`` replays the prefill graph captured beforehand for
+the prompt length (``ttft_eager_ms``: the same prefill issued kernel by
+kernel); the token ids are copied from the host inside both timings. Every
+config also prints the reference's ``Latency (us):`` / ``Effective
+Bandwidth:`` lines on stderr.
 """
 
 from __future__ import annotations
@@ -169,14 +189,22 @@ def _check(lib, rc):
         raise RuntimeError(lib.iron_last_error().decode())
 
 
-def bench_gemv_int4(torch, lib, tm, dev, steps, warmup):
-    """The headline: `steps` launches of the config 2 GEMV, timed as graph replays
-    that follow the cache-proof rotation (Timer): a graph G of one launch per
-    weight copy (every copy once, in order) is replayed once warm, then the
-    timed region is q replays of G plus one graph of the remaining r launches
-    (steps = q * copies + r), so every timed launch reads a copy that
-    `copies - 1` other launches (>= POOL_BYTES) have read past since its last use."""
+def bench_gemv_int4(torch, lib, tm, dev, steps, warmup, rounds=5):
+    """The headline: `steps` launches of the config 2 GEMV, timed on the GPU
+    without any graph boundary inside the measurement.
+
+    Two graphs are captured: `lead`, one launch per weight copy (every copy
+    once, in rotation order), and `full`, the same lead followed by the
+    `steps` timed launches, which continue the rotation (so every timed
+    launch reads a copy that `copies - 1` other launches, >= POOL_BYTES, have
+    read past since its last use). Each is replayed behind an untimed replay
+    of `lead` that keeps the GPU busy while the host queues it, and the timed
+    region is the difference of the two replay times: the device time of
+    exactly the `steps` launches. A graph replay carries a fixed cost of
+    several microseconds at its start and end; the difference cancels it, so
+    the per-launch time does not depend on `steps`. Median over `rounds`."""
     from iron_amd import _lib
+    from iron_amd.common.graph import capture_graph
     from oracle import configs
 
     M, K = 8192, 2048
@@ -197,19 +225,18 @@ def bench_gemv_int4(torch, lib, tm, dev, steps, warmup):
 
     for i in range(warmup):
         launch(i, stream)
-    full = tm.capture(launch, copies)
-    q, r = divmod(steps, copies)
-    tail = tm.capture(launch, r) if r else None
+    lead = tm.capture(launch, copies)
+    full = tm.capture(launch, copies + steps)
     full.replay()
-    # timed: q replays of the full rotation + the tail, after an untimed lead
-    # replay of the full rotation (every copy read once, in order)
-    wall = tm.replay_ms([full] * q + ([tail] if tail else []), lead=full)
-    del full, tail
+    t_lead = sorted(tm.replay_ms([lead], lead=lead) for _ in range(rounds))[rounds // 2]
+    t_full = sorted(tm.replay_ms([full], lead=lead) for _ in range(rounds))[rounds // 2]
+    wall = t_full - t_lead
+    del lead, full
     # the same kernel issued one Python call at a time (host-bound when the kernel is short)
     n_py = min(steps, 1000)
     py_us = tm.wall_ms(launch, n_py) * 1e3 / n_py
     return {"bytes": nbytes, "wall_ms": wall, "copies": copies, "python_launch_us": py_us,
-            "launches_per_graph": copies, "tail_launches": r,
+            "lead_ms": t_lead, "full_ms": t_full,
             "timed_distinct_bytes": min(steps, copies) * (codes.numel() + 2 * scales.numel()),
             "inputs": (codes, scales, x)}
 
@@ -470,7 +497,8 @@ def bench_floor(torch, lib, tm, dev):
         out["empty_graph_node_us"][str(wgs)] = round(tm.rotating_us(empty, 1, 500), 3)
         out["empty_python_launch_us"][str(wgs)] = round(tm.wall_ms(empty, 500) * 1e3 / 500, 3)
     sizes = {"cfg2_int4_gemv": 9457664, "cfg3_gqa_kv": 4194304, "kv4096_layer": 8388608,
-             "cfg1_bf16_gemv": 33574912}
+             "cfg1_bf16_gemv": 33574912, "swiglu_int4_pair": 18874368, "lm_head_bf16": 525336576,
+             "stream_1GiB": 1 << 30}
     for name, nbytes in sizes.items():
         stride = (nbytes + 255) // 256 * 256
         copies = copies_for(stride)
@@ -486,7 +514,7 @@ def bench_floor(torch, lib, tm, dev):
                 _check(lib, lib.iron_probe_read(base + (i % copies) * stride, nbytes, sink.data_ptr(), wgs, lpl, s))
 
             read(0, _lib.stream_handle(dev))
-            t = tm.rotating_us(read, copies, 200)
+            t = tm.rotating_us(read, copies, 200 if nbytes < (64 << 20) else 2 * copies)
             row[f"loads_per_lane_{lpl}"] = {"us": round(t, 3), "GB/s": round(nbytes / t / 1e3, 1)}
         best = min(v["us"] for v in row.values())
         out["read_us"][name] = {"bytes": nbytes, "best_us": best, "best_GB/s": round(nbytes / best / 1e3, 1),
@@ -722,8 +750,11 @@ def main() -> int:
             "weight_pool_copies": i4["copies"],
             "algorithmic_bytes_per_step": i4["bytes"],
             "timed_distinct_bytes": i4["timed_distinct_bytes"],
-            "launches_per_graph_replay": i4["launches_per_graph"],
-            "tail_graph_launches": i4["tail_launches"],
+            "timing": "device time of the steps launches = replay time of one graph holding a lead of "
+            "weight_pool_copies launches then the steps launches, minus the replay time of the lead alone "
+            "(medians of 5)",
+            "lead_replay_ms": round(i4["lead_ms"], 4),
+            "lead_plus_steps_replay_ms": round(i4["full_ms"], 4),
             "python_launch_us": round(i4["python_launch_us"], 3),
         },
         "roofline": {

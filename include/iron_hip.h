@@ -48,7 +48,13 @@ enum iron_epilogue {
   IRON_EPI_GELU_TANH = 1,
   IRON_EPI_SILU = 2,
   IRON_EPI_SIGMOID = 3,
-  IRON_EPI_GELU_SIGMOID = 4
+  IRON_EPI_GELU_SIGMOID = 4,
+  /* OR'ed into the epilogue code of the GEMM entry points: every fp32 -> bf16
+   * conversion of the output stage (before the activation and at the store)
+   * truncates the mantissa -- rounds toward zero -- instead of rounding to
+   * nearest even: flm.GEMM(rounding="floor"), iron/operators/flm/gemm/
+   * op.py:105,426-430 and design.py:164-172. */
+  IRON_EPI_ROUND_TOWARD_ZERO = 0x100
 };
 
 /* ---------------------------------------------------------------- GEMV ---- */

@@ -58,6 +58,14 @@ constexpr int kSplitTile = 128;  // tile edge the split-K policy counts in
 // public enum: B rows come in 64-row blocks alternating gate / up.
 constexpr int kEpiSwigluPair = 100;
 
+// bf16 of x for the output stage: round to nearest even, or toward zero
+// (mantissa truncation, flm.GEMM's "floor" conversion); NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t out_bf16(float x, int toward_zero) {
+  if (!toward_zero) return f32_to_bf16(x);
+  const uint32_t u = __float_as_uint(x);
+  return static_cast<uint16_t>(x != x ? (u >> 16) | 0x40u : u >> 16);
+}
+
 struct GemmArgs {
   const uint16_t* A;  // (M, K)
   const uint16_t* B;  // (N, K)
@@ -74,7 +82,15 @@ struct GemmArgs {
   const uint8_t* codes;
   const uint16_t* scales;
   int is_signed;
+  int toward_zero;  // output-stage conversions truncate instead of rounding to nearest even
 };
+
+// Splits an entry point's epilogue code into the activation (a.epi) and the
+// IRON_EPI_ROUND_TOWARD_ZERO flag (a.toward_zero).
+static void set_epilogue(GemmArgs& a, int epilogue) {
+  a.toward_zero = (epilogue & IRON_EPI_ROUND_TOWARD_ZERO) != 0;
+  a.epi = epilogue & ~IRON_EPI_ROUND_TOWARD_ZERO;
+}
 
 template <int WMW_, int WNW_, int TI_, int TJ_, int NS_>
 struct Tile {
@@ -142,11 +158,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
         const int col = wn * TJ * 32 + j * 32 + (lane & 31);
         float x = acc[i][j][v];
         if (!swiglu && (a.epi != EPI_NONE || a.clamp)) {
-          x = bf16_to_f32(f32_to_bf16(x));
+          x = bf16_to_f32(out_bf16(x, a.toward_zero));
           x = apply_epilogue(x, a.epi);
           if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
         }
-        Cs[row * BN + col] = f32_to_bf16(x);
+        Cs[row * BN + col] = out_bf16(x, a.toward_zero);
       }
   __syncthreads();
   if (swiglu) {
@@ -501,12 +517,12 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(GemmArgs a) {
   float x = 0.f;
   for (int kb = 0; kb < a.splits; ++kb) x += a.partial[kb * mn + t];
   if (a.epi != EPI_NONE || a.clamp) {
-    x = bf16_to_f32(f32_to_bf16(x));
+    x = bf16_to_f32(out_bf16(x, a.toward_zero));
     x = apply_epilogue(x, a.epi);
     if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
   }
   const long long m = t / a.N, n = t % a.N;
-  a.C[m * a.ldc + n] = f32_to_bf16(x);
+  a.C[m * a.ldc + n] = out_bf16(x, a.toward_zero);
 }
 
 // The same merge, 8 outputs per thread: 16-byte loads of every K range issued
@@ -545,14 +561,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce8_kernel(GemmArgs a) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     if (a.epi != EPI_NONE || a.clamp) {
-      x[e] = bf16_to_f32(f32_to_bf16(x[e]));
+      x[e] = bf16_to_f32(out_bf16(x[e], a.toward_zero));
       x[e] = apply_epilogue(x[e], a.epi);
       if (a.clamp) x[e] = fminf(fmaxf(x[e], a.lo), a.hi);
     }
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    h[e] = static_cast<uint32_t>(f32_to_bf16(x[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(x[2 * e + 1])) << 16);
+    h[e] = static_cast<uint32_t>(out_bf16(x[2 * e], a.toward_zero)) |
+           (static_cast<uint32_t>(out_bf16(x[2 * e + 1], a.toward_zero)) << 16);
   *reinterpret_cast<uint4*>(a.C + static_cast<size_t>(m) * a.ldc + 8 * c) = make_uint4(h[0], h[1], h[2], h[3]);
 }
 
@@ -593,7 +610,8 @@ static int gemm_check(const char* fn, const void* A, const void* B, const void* 
   IRON_REQUIRE(K % BK == 0, "%s: K=%d must be a multiple of %d", fn, K, BK);
   IRON_REQUIRE(aligned16(A) && aligned16(B), "%s: A and B must be 16-byte aligned", fn);
   IRON_REQUIRE(ldc >= N, "%s: ldc=%lld < N=%d", fn, ldc, N);
-  IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "%s: bad epilogue %d", fn, epilogue);
+  const int act = epilogue & ~IRON_EPI_ROUND_TOWARD_ZERO;
+  IRON_REQUIRE(act >= EPI_NONE && act <= EPI_GELU_SIGMOID, "%s: bad epilogue %d", fn, epilogue);
   IRON_REQUIRE(!has_clamp || clamp_lo <= clamp_hi, "%s: clamp min > max", fn);
   if ((ldc % 8 == 0) && !aligned16(C)) return fail_einval("%s: C must be 16-byte aligned", fn);
   return 0;
@@ -654,6 +672,7 @@ extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, i
   IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt: problem too large");
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, nullptr, 1};
+  set_epilogue(a, epilogue);
   gemm_launch(a, static_cast<hipStream_t>(stream));
   return check_launch("gemm_bf16_nt");
 }
@@ -692,6 +711,7 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
                "iron_gemm_bf16_nt_splitk: problem too large");
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, static_cast<float*>(workspace), splits};
+  set_epilogue(a, epilogue);
   hipStream_t s = static_cast<hipStream_t>(stream);
   gemm_launch(a, s);
   launch_splitk_reduce(a, s);
@@ -747,6 +767,7 @@ extern "C" int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* 
   GemmArgs a{static_cast<const uint16_t*>(A), nullptr, static_cast<uint16_t*>(C), M, N, K, ldc, epilogue, has_clamp,
              clamp_lo, clamp_hi, partial, splits, static_cast<const uint8_t*>(codes),
              static_cast<const uint16_t*>(scales), is_signed ? 1 : 0};
+  set_epilogue(a, epilogue);
   hipStream_t s = static_cast<hipStream_t>(stream);
   gemm_i4_launch(a, s);
   if (splits > 1) launch_splitk_reduce(a, s);

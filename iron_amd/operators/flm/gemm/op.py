@@ -8,8 +8,10 @@ before the activation, as the reference kernel does.
 ``pack_B(B)`` reorders a row-major (K, N) weight once into the kernel's
 consumption order, here (N, K) K-contiguous; the arg spec is
 (A (M, K), B packed (N, K), C (M, N)). The AIE tiling knobs (tile_n, k_tile,
-tile_ma, m_chunk, rounding) are accepted for API compatibility; rounding is
-always round-to-nearest-even.
+tile_ma, m_chunk) are accepted for API compatibility. ``rounding`` selects
+the fp32 -> bf16 conversions of the output stage (design.py:164-172):
+``conv_even`` rounds to nearest even, ``floor`` truncates the mantissa
+(rounds toward zero), the reference's overlay mode (op.py:105,426-430).
 """
 
 from dataclasses import dataclass, field
@@ -48,6 +50,7 @@ class Rounding(str, Enum):
 
 # kernel epilogue codes (include/iron_hip.h: enum iron_epilogue)
 _EPI_CODE = {Epilogue.NONE: 0, Epilogue.GELU: 4, Epilogue.SILU: 2, Epilogue.SIGMOID: 3}
+_ROUND_TOWARD_ZERO = 0x100  # IRON_EPI_ROUND_TOWARD_ZERO
 K_TILE = 512
 
 
@@ -98,8 +101,6 @@ class GEMM(HIPOperator):
             lo, hi = self.clamp
             if lo > hi:
                 raise ValueError(f"clamp min ({lo}) must be <= max ({hi})")
-        if self.rounding is not Rounding.CONV_EVEN:
-            raise ValueError("only round-to-nearest-even conversion is implemented")
         self._ws = {}
         HIPOperator.__init__(self, context=self.context)
 
@@ -122,6 +123,8 @@ class GEMM(HIPOperator):
     def _launch(self, A, B, C, *, stream):
         lo, hi = (float(self.clamp[0]), float(self.clamp[1])) if self.clamp is not None else (0.0, 0.0)
         epi, has_clamp = _EPI_CODE[self.epilogue], int(self.clamp is not None)
+        if self.rounding is Rounding.FLOOR:
+            epi |= _ROUND_TOWARD_ZERO
         splits = _lib.query("iron_gemm_splitk_choose", self.M, self.N, self.K)
         if splits > 1:  # output tiles alone cannot fill the GPU: split K, merge applies the epilogue
             need = int(_lib.query("iron_gemm_splitk_workspace_bytes", self.M, self.N, splits))

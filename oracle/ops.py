@@ -391,8 +391,24 @@ def gemm_golden(M, K, N, seed=42, b_col_maj=False):
 FLM_EPILOGUES = ("none", "gelu", "silu", "sigmoid")
 
 
-def flm_apply_epilogue(C, epilogue="none", clamp=None):
-    """flm.GEMM output stage (flm/gemm/reference.py:8-31); gelu = x*sigmoid(1.702x)."""
+def bf16_toward_zero(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> bf16 by mantissa truncation (round toward zero): the "floor"
+    conversion of flm.GEMM (flm/gemm/design.py:164-172). NaN stays NaN.
+    PINNED BY: known answers and the truncation invariants (|y| <= |x|, same
+    sign, |x - y| < one bf16 ulp) in tests/test_oracle_ops.py."""
+    x = x.float().contiguous()
+    bits = x.view(torch.int32) & ~0xFFFF
+    y = bits.view(torch.float32).to(BF16)  # exact: the low 16 bits are zero
+    return torch.where(torch.isnan(x), torch.full_like(y, float("nan")), y)
+
+
+def _to_bf16(x: torch.Tensor, rounding: str) -> torch.Tensor:
+    return bf16_toward_zero(x) if rounding == "floor" else x.to(BF16)
+
+
+def flm_apply_epilogue(C, epilogue="none", clamp=None, rounding="conv_even"):
+    """flm.GEMM output stage (flm/gemm/reference.py:8-31); gelu = x*sigmoid(1.702x).
+    With rounding="floor" the final bf16 conversion truncates."""
     Cf = C.float()
     if epilogue == "gelu":
         Cf = Cf * torch.sigmoid(1.702 * Cf)
@@ -404,21 +420,22 @@ def flm_apply_epilogue(C, epilogue="none", clamp=None):
         raise ValueError(epilogue)
     if clamp is not None:
         Cf = torch.clamp(Cf, clamp[0], clamp[1])
-    return Cf.to(C.dtype)
+    return _to_bf16(Cf, rounding)
 
 
-def flm_gemm_reference(A, B, epilogue="none", clamp=None):
-    """fp32 matmul -> bf16 -> epilogue -> clamp (flm/gemm/reference.py:34-57)."""
-    C = torch.matmul(A.float(), B.float()).to(A.dtype)
-    return flm_apply_epilogue(C, epilogue, clamp)
+def flm_gemm_reference(A, B, epilogue="none", clamp=None, rounding="conv_even"):
+    """fp32 matmul -> bf16 -> epilogue -> clamp (flm/gemm/reference.py:34-57).
+    rounding="floor": both bf16 conversions truncate (flm/gemm/op.py:105)."""
+    C = _to_bf16(torch.matmul(A.float(), B.float()), rounding)
+    return flm_apply_epilogue(C, epilogue, clamp, rounding)
 
 
-def flm_gemm_golden(M, K, N, seed=42, epilogue="none", clamp=None, scale=4.0):
+def flm_gemm_golden(M, K, N, seed=42, epilogue="none", clamp=None, scale=4.0, rounding="conv_even"):
     """Seeded inputs of flm/gemm/reference.py:60-81."""
     torch.manual_seed(seed)
     A = torch.randn(M, K, dtype=BF16) * scale
     B = torch.rand(K, N, dtype=BF16) * scale
-    return {"input": A, "input_b": B, "output": flm_gemm_reference(A, B, epilogue, clamp)}
+    return {"input": A, "input_b": B, "output": flm_gemm_reference(A, B, epilogue, clamp, rounding)}
 
 
 # ------------------------------------------------------------------ SwiGLU

@@ -296,3 +296,50 @@ def test_gemm_swiglu_matches_unfused(gpu, M, K, F):
     assert rel_l2 <= 1e-2 and max_abs <= 2e-2 * max(1.0, float(ref.abs().max())), (max_abs, rel_l2)
     with pytest.raises(RuntimeError, match="multiple of 64"):
         _lib.call("iron_gemm_bf16_nt_swiglu", Ad.data_ptr(), Wgu.data_ptr(), H.data_ptr(), M, F + 32, K, F + 32, s)
+
+
+@pytest.mark.parametrize("M,K,N,epilogue,clamp", [(256, 512, 1024, "none", None), (256, 512, 1024, "silu", None),
+                                                  (64, 2048, 512, "none", (-50.0, 50.0)), (512, 2048, 2048, "gelu", None)])
+def test_flm_gemm_floor_rounding(gpu, M, K, N, epilogue, clamp):
+    """flm.GEMM(rounding="floor") (flm/gemm/op.py:105,426-430; the reference's
+    test list carries it at 256x512x1024): every output-stage conversion
+    truncates. Against the oracle's truncating golden within one bf16 ulp (the
+    fp32 sums differ in order, so a value next to a boundary may land one ulp
+    apart), and against the same GEMM with round-to-nearest: never larger in
+    magnitude, different in a large share of the elements. The last shape
+    splits K (the merge kernel's conversions)."""
+    from iron_amd.operators import flm
+
+    scale = 4.0 if epilogue == "none" else 0.5
+    g = ops.flm_gemm_golden(M, K, N, epilogue=epilogue, clamp=clamp, scale=scale, rounding="floor")
+    outs = {}
+    for rnd in ("conv_even", "floor"):
+        op = flm.GEMM(M=M, K=K, N=N, epilogue=epilogue, clamp=clamp, rounding=rnd)
+        C = torch.empty(M, N, dtype=BF16, device=gpu)
+        op.get_callable()(g["input"].to(gpu), op.pack_B(g["input_b"]).to(gpu), C)
+        torch.cuda.synchronize()
+        outs[rnd] = C.cpu().float()
+    fl, rne = outs["floor"], outs["conv_even"]
+    if epilogue == "none" and clamp is None:
+        assert torch.all(fl.abs() <= rne.abs())
+        assert (fl != rne).float().mean() > 0.2
+    else:
+        assert (fl != rne).float().mean() > 0.05
+    if epilogue == "none":
+        bad = ops.within_bf16_ulps(fl.to(BF16), g["output"].float(), n_ulp=1.0, atol=1e-6)
+    else:
+        # the fp32 accumulators differ by the summation order (up to ~2^-20 of the
+        # element's mass sum |a||b|, which dominates where the sum cancels to near
+        # zero), so the first conversion may land one ulp of the accumulator or
+        # that much apart; the activation (slope <= 1.13 for silu and
+        # x*sigmoid(1.702x)) carries it into the output, truncated once more
+        acc = g["input"].float() @ g["input_b"].float()
+        mass = g["input"].float().abs() @ g["input_b"].float().abs()
+        d = (fl - g["output"].float()).abs().reshape(-1)
+        allowed = (1.2 * (ops.bf16_ulp(acc) + 2.0**-20 * mass.double()) + ops.bf16_ulp(g["output"].float()))
+        allowed = allowed.reshape(-1).float()
+        bad = torch.nonzero(d > allowed).flatten().tolist()
+        detail = [(i, float(fl.reshape(-1)[i]), float(g["output"].float().reshape(-1)[i]), float(acc.reshape(-1)[i]),
+                   float(rne.reshape(-1)[i])) for i in bad[:5]]
+        assert not bad, detail
+    assert not bad, bad[:5]

@@ -271,3 +271,40 @@ def test_repeat_and_transpose_references():
     assert ops.repeat_reference(x, 2).tolist() == [r for r in x.tolist() for _ in range(2)]
     t = ops.transpose_reference(torch.arange(24.0), 4, 6)
     assert torch.equal(t[0], torch.arange(24.0).reshape(4, 6).T)
+
+
+def test_bf16_toward_zero_known_answers_and_invariants():
+    """The oracle's "floor" conversion of flm.GEMM (flm/gemm/design.py:164-172:
+    truncation, which the reference describes as biasing every conversion the
+    same way): the mantissa is cut, so the result rounds toward zero -- for a
+    negative value that is up, not down (-1.01171875 -> -1.0078125)."""
+    x = torch.tensor([1.01171875, -1.01171875, 1.00390625, 1.0, -0.0, 3.3895313892515355e38, float("inf"),
+                      float("-inf"), 1e-40, float("nan")], dtype=torch.float32)
+    y = ops.bf16_toward_zero(x).float()
+    want = [1.0078125, -1.0078125, 1.0, 1.0, -0.0, 3.3895313892515355e38, float("inf"), float("-inf")]
+    assert y[:8].tolist() == want
+    assert x[2].to(torch.bfloat16).float() == 1.0 and x[0].to(torch.bfloat16).float() == 1.015625  # RNE differs
+    assert 0 <= y[8] <= 1e-40 and torch.isnan(y[9])
+    g = torch.Generator().manual_seed(0)
+    r = torch.randn(100000, generator=g) * torch.exp(torch.randn(100000, generator=g) * 8)
+    t = ops.bf16_toward_zero(r).float()
+    assert torch.all(t.abs() <= r.abs()) and torch.all((t == 0) | (torch.sign(t) == torch.sign(r)))
+    # the largest-magnitude bf16 not above |r|: the RNE neighbour, or the one below it toward zero
+    rne = r.to(torch.bfloat16).float()
+    below = torch.where(rne.abs() > r.abs(), torch.nextafter(rne.to(torch.bfloat16), torch.zeros(1, dtype=torch.bfloat16)).float(), rne)
+    assert torch.equal(t, below)
+    exact = r.to(torch.bfloat16).float()
+    assert torch.equal(ops.bf16_toward_zero(exact).float(), exact)  # bf16 values pass unchanged
+
+
+def test_flm_gemm_floor_reference():
+    """flm_gemm_reference(rounding="floor") truncates both conversions: its
+    outputs never exceed the round-to-nearest ones in magnitude and differ from
+    them in a large share of the elements."""
+    g = ops.flm_gemm_golden(64, 512, 96, epilogue="none", rounding="floor")
+    rne = ops.flm_gemm_reference(g["input"], g["input_b"])
+    fl = g["output"].float()
+    assert torch.all(fl.abs() <= rne.float().abs())
+    assert (fl != rne.float()).float().mean() > 0.2
+    acc = g["input"].float() @ g["input_b"].float()
+    assert torch.equal(g["output"], ops.bf16_toward_zero(acc))
