@@ -77,7 +77,7 @@ METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 # HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE +
 # WRITE_SIZE, each scaled by the counter's reading for a copy of known size
 # (profiles/gemv_i4g32_cfg2_pmc.md).
-TRAFFIC_BYTES = 9551129
+TRAFFIC_BYTES = 9551390
 
 
 def copies_for(nbytes: int) -> int:
@@ -523,6 +523,44 @@ def bench_floor(torch, lib, tm, dev):
     return out
 
 
+def bench_mfma(torch, lib, tm, dev):
+    """MFMA issue rate and shader clock (iron_probe_mfma): register-only
+    v_mfma_f32_32x32x16_bf16 loops, first with the config 5 prefill GEMM's
+    per-CU work (256 workgroups of 8 waves, 256 MFMAs per wave on 2
+    accumulators, as its 128x128 tile issues over K = 2048), then variants.
+    Per case: graph-replayed time per launch, achieved TFLOP/s, and from the
+    in-kernel clock stamps the median shader clock (MHz) and shader cycles per
+    wave."""
+    from iron_amd import _lib
+
+    cases = [("cfg5_gemm_tile", 256, 8, 256, 2), ("cfg5_4chains", 256, 8, 256, 4), ("cfg5_8chains", 256, 8, 256, 8),
+             ("1wave_per_simd", 256, 4, 512, 2), ("1wave_per_simd_4chains", 256, 4, 512, 4),
+             ("steady_2x", 512, 8, 2048, 4), ("steady_4x", 1024, 8, 2048, 4)]
+    out = {}
+    for name, wgs, wpw, n, chains in cases:
+        waves = wgs * wpw
+        sink = torch.empty(waves, dtype=torch.float32, device=dev)
+        clocks = torch.zeros(waves * 4, dtype=torch.int64, device=dev)
+
+        def run(i, s, wgs=wgs, wpw=wpw, n=n, chains=chains, sink=sink, clocks=clocks, waves=waves):
+            _check(lib, lib.iron_probe_mfma(wgs, wpw, n, chains, sink.data_ptr(), clocks.data_ptr(), waves, s))
+
+        run(0, _lib.stream_handle(dev))
+        t = tm.rotating_us(run, 1, 20)
+        torch.cuda.synchronize()
+        c = clocks.view(waves, 4).cpu().double()
+        cyc = (c[:, 1] - c[:, 0])
+        real_s = (c[:, 3] - c[:, 2]) / 100e6
+        mhz = (cyc / real_s.clamp_min(1e-9) / 1e6).median().item()
+        flops = 2.0 * 32 * 32 * 16 * n * waves
+        out[name] = {"workgroups": wgs, "waves_per_wg": wpw, "mfma_per_wave": n, "chains": chains,
+                     "kernel_us": round(t, 3), "TFLOP/s": round(flops / t / 1e6, 1),
+                     "frac_mfma": round(flops / t / 1e6 / BF16_PEAK_TFLOPS, 4),
+                     "shader_MHz_median": round(mhz, 1), "wave_cycles_median": int(cyc.median().item()),
+                     "wave_us_median": round(float(real_s.median().item()) * 1e6, 3)}
+    return out
+
+
 def bench_model(torch, dev, decode_steps=128, prompt_len=512, long_ctx=3968):
     """Config 5: random-init Llama-3.2-1B shape, int4-g32 linears, bf16 tied head."""
     from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
@@ -684,7 +722,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
-    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill", "attention", "floor"], default="full")
+    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill", "attention", "floor", "mfma"],
+                    default="full")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -725,6 +764,8 @@ def main() -> int:
         })
     if args.mode == "floor":
         return emit("floor", {"floor": bench_floor(torch, lib, tm, dev)})
+    if args.mode == "mfma":
+        return emit("mfma", {"mfma": bench_mfma(torch, lib, tm, dev)})
 
     i4 = bench_gemv_int4(torch, lib, tm, dev, args.steps, args.warmup)
     value = i4["bytes"] * args.steps / (i4["wall_ms"] * 1e-3) / 1e9

@@ -392,6 +392,15 @@ long long iron_probe_read_workgroups(long long nbytes, int loads_per_lane);
 int iron_probe_read(const void* src, long long nbytes, void* sink, long long sink_words, int loads_per_lane,
                     void* stream);
 
+/* MFMA-only loop: every wave of workgroups x waves_per_workgroup issues
+ * mfma_per_wave v_mfma_f32_32x32x16_bf16 over `chains` (1,2,4,8) independent
+ * accumulators, register operands only. Per wave w: sink[w] (float) = sum of
+ * the accumulators, clocks[4w..4w+3] (uint64) = shader clock (s_memtime)
+ * before, after, 100 MHz real-time counter (s_memrealtime) before, after.
+ * sink and clocks hold waves_capacity waves. */
+int iron_probe_mfma(int workgroups, int waves_per_workgroup, int mfma_per_wave, int chains, void* sink, void* clocks,
+                    long long waves_capacity, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

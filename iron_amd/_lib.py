@@ -60,6 +60,7 @@ SIGNATURES: dict[str, list] = {
     "iron_gemm_nt_partials": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _LL, _P],
     "iron_probe_empty": [_I, _P],
     "iron_probe_read": [_P, _LL, _P, _LL, _I, _P],
+    "iron_probe_mfma": [_I, _I, _I, _I, _P, _P, _LL, _P],
 }
 
 # ... except these queries, which return a value.

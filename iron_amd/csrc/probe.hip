@@ -1,9 +1,11 @@
-// Measurement probes for the launch and read floors that bound the short
-// decode kernels: an empty kernel (what one launch, or one node of a replayed
-// hipGraph, costs with no work) and a pure streaming read of n bytes (what
-// the memory system delivers to one launch of that size, with no arithmetic
-// and no stores beyond one word per workgroup). bench.py --mode floor times
-// both under the same graph protocol as the kernels they bound.
+// Measurement probes for the floors that bound the kernels: an empty kernel
+// (what one launch, or one node of a replayed hipGraph, costs with no work),
+// a pure streaming read of n bytes (what the memory system delivers to one
+// launch of that size, with no arithmetic and no stores beyond one word per
+// workgroup), and an MFMA-only loop with clock stamps (the matrix cores' issue
+// rate and the shader clock under that load). bench.py --mode floor and
+// --mode mfma run them under the same graph protocol as the kernels they
+// bound.
 #include "iron_common.hpp"
 #include "../../include/iron_hip.h"
 
@@ -44,10 +46,81 @@ __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const uint4*
   }
 }
 
+typedef __bf16 probe_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float probe_f32x16 __attribute__((ext_vector_type(16)));
+
+// MFMA issue probe: every wave issues n_mfma v_mfma_f32_32x32x16_bf16 over
+// CHAINS independent accumulators (register operands only: no loads, no LDS),
+// as the GEMM's wave tile does per K step, and lane 0 records the shader clock
+// (s_memtime) and the 100 MHz real-time counter (s_memrealtime) before and
+// after, so the host reads the cycles per MFMA and the clock the SIMDs ran at.
+// The accumulators are summed into sink[wave] so that the MFMAs are live.
+template <int CHAINS>
+__global__ void mfma_probe_kernel(int n_mfma, float* __restrict__ sink, unsigned long long* __restrict__ clocks) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  probe_bf16x8 av, bv;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    av[e] = static_cast<__bf16>(static_cast<float>((lane + e) % 7) * 0.125f);
+    bv[e] = static_cast<__bf16>(static_cast<float>((lane * 3 + e) % 5) * 0.25f);
+  }
+  probe_f32x16 acc[CHAINS];
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.f;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < n_mfma; i += CHAINS) {
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc[c], 0, 0, 0);
+  }
+  float t = 0.f;
+#pragma unroll
+  for (int c = 0; c < CHAINS; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) t += acc[c][v];
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  t = wave_sum(t);
+  if (lane == 0) {
+    sink[wave] = t;
+    clocks[4 * wave] = t0;
+    clocks[4 * wave + 1] = t1;
+    clocks[4 * wave + 2] = r0;
+    clocks[4 * wave + 3] = r1;
+  }
+}
+
 }  // namespace
 }  // namespace iron
 
 using namespace iron;
+
+extern "C" int iron_probe_mfma(int workgroups, int waves_per_workgroup, int mfma_per_wave, int chains, void* sink,
+                               void* clocks, long long waves_capacity, void* stream) {
+  IRON_REQUIRE(sink && clocks, "iron_probe_mfma: null pointer");
+  IRON_REQUIRE(workgroups > 0 && workgroups <= 65536 && waves_per_workgroup > 0 && waves_per_workgroup <= 16,
+               "iron_probe_mfma: workgroups=%d (1..65536), waves_per_workgroup=%d (1..16)", workgroups,
+               waves_per_workgroup);
+  IRON_REQUIRE(chains == 1 || chains == 2 || chains == 4 || chains == 8, "iron_probe_mfma: chains=%d not in {1,2,4,8}",
+               chains);
+  IRON_REQUIRE(mfma_per_wave > 0 && mfma_per_wave % chains == 0,
+               "iron_probe_mfma: mfma_per_wave=%d must be a positive multiple of chains", mfma_per_wave);
+  IRON_REQUIRE(static_cast<long long>(workgroups) * waves_per_workgroup <= waves_capacity,
+               "iron_probe_mfma: sink/clocks hold %lld waves, %lld needed", waves_capacity,
+               static_cast<long long>(workgroups) * waves_per_workgroup);
+  const dim3 grid(workgroups), block(waves_per_workgroup * kWave);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* sk = static_cast<float*>(sink);
+  unsigned long long* ck = static_cast<unsigned long long*>(clocks);
+  switch (chains) {
+    case 1: IRON_LAUNCH(mfma_probe_kernel<1>, grid, block, 0, s, mfma_per_wave, sk, ck); break;
+    case 2: IRON_LAUNCH(mfma_probe_kernel<2>, grid, block, 0, s, mfma_per_wave, sk, ck); break;
+    case 4: IRON_LAUNCH(mfma_probe_kernel<4>, grid, block, 0, s, mfma_per_wave, sk, ck); break;
+    default: IRON_LAUNCH(mfma_probe_kernel<8>, grid, block, 0, s, mfma_per_wave, sk, ck); break;
+  }
+  return check_launch("probe_mfma");
+}
 
 extern "C" int iron_probe_empty(int workgroups, void* stream) {
   IRON_REQUIRE(workgroups > 0 && workgroups <= (1 << 20), "iron_probe_empty: workgroups=%d outside [1, 2^20]",
