@@ -183,12 +183,18 @@ int iron_rope(const void* x, const void* angles, int angles_fp32, void* out, int
 
 /* ----------------------------------------------------------- Attention ---- */
 
-/* Bytes of workspace iron_gqa_decode needs for this shape (-1 if invalid).
- * Scratch for the per-chunk partial results (no initialisation needed); calls
- * that share one workspace must be stream-ordered. */
+/* Bytes of workspace iron_gqa_decode needs for this shape (-1 if invalid):
+ * one arrival counter per KV head (a 128-byte line each), then the per-chunk
+ * partial results. Zero-fill it once before the first call: the counters must
+ * start at zero, and every call leaves them at zero. Calls that share one
+ * workspace must be stream-ordered, and nothing else may write to it between
+ * calls. */
 long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
 
-/* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}):
+/* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}).
+ * With n_kv_heads a multiple of 8 it is one kernel launch (each KV head's
+ * chunks run on one XCD and the last of them to finish merges them there),
+ * otherwise two (chunk partials, then a merge kernel):
  *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
  *                                               (angle_rows, 64) [cos,sin])
  *   k_cache[:, pos] = k', v_cache[:, pos] = v_new
@@ -203,8 +209,8 @@ int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k
                     const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
                     int head_dim, int max_len, int pos, const int* pos_dev, float scale, void* stream);
 
-/* iron_gqa_decode without a workspace argument: the partials go to a scratch
- * array the library holds in device memory, one per GPU, for the life of the
+/* iron_gqa_decode without a workspace argument: the counters and partials go
+ * to a scratch array the library holds in device memory, one per GPU, for the life of the
  * process (iron_gqa_decode_noalloc_max_bytes(), 4 MiB: at the Llama-3.2-1B
  * shape, 32/8 heads, up to max_len 31744). It allocates nothing, so callers
  * that cannot allocate device memory (code under hipGraph capture, tight
@@ -212,8 +218,10 @@ int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k
  * iron_gqa_decode_workspace_bytes() exceed the maximum are rejected
  * (IRON_EINVAL) before anything runs. Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race;
- * stream-ordered calls are safe. The array needs no initialisation (every
- * partial is written before it is read). Same results as iron_gqa_decode.
+ * stream-ordered calls are safe. Each call first zeroes the array's arrival
+ * counters (a one-wave kernel; with n_kv_heads not a multiple of 8 there are
+ * none), so nothing carries over from an earlier call, racing or not. Same
+ * results as iron_gqa_decode.
  * No counterpart in the reference: it exists for the callers above. */
 long long iron_gqa_decode_noalloc_max_bytes(void);
 int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -400,6 +408,12 @@ int iron_probe_read(const void* src, long long nbytes, void* sink, long long sin
  * sink and clocks hold waves_capacity waves. */
 int iron_probe_mfma(int workgroups, int waves_per_workgroup, int mfma_per_wave, int chains, void* sink, void* clocks,
                     long long waves_capacity, void* stream);
+
+/* XCD of each workgroup of a launch of `workgroups` x 256 threads (the
+ * hardware register XCC_ID, one int per workgroup into ids). The one-launch
+ * GQA decode relies on workgroups whose linear ids agree mod 8 sharing an
+ * XCD; this shows it on the device at hand. */
+int iron_probe_xcc_ids(int workgroups, void* ids, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,7 @@ SIGNATURES: dict[str, list] = {
     "iron_probe_empty": [_I, _P],
     "iron_probe_read": [_P, _LL, _P, _LL, _I, _P],
     "iron_probe_mfma": [_I, _I, _I, _I, _P, _P, _LL, _P],
+    "iron_probe_xcc_ids": [_I, _P, _P],
 }
 
 # ... except these queries, which return a value.

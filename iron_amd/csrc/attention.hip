@@ -1,16 +1,19 @@
-// GQA attention for decode (split-K flash-decode in one kernel) and causal prefill.
+// GQA attention for decode (split-K flash-decode) and causal prefill.
 //
 // Decode: one new token. A workgroup owns (KV head j, a chunk of 64 cache
 // positions) and serves the G = H/Hkv query heads that share KV head j, so
 // every K/V byte is read from HBM once for all of them. Inside the chunk the
-// softmax is exact in fp32 (scores scaled by log2(e)/sqrt(D), exp2); the
-// chunk's unnormalised output, maximum and sum go to a workspace, and a second
-// small kernel merges the chunks. (Merging in the last-arriving workgroup was
-// measured slower: cross-XCD visibility of the partials needs either an
-// agent-scope release, which writes back the whole per-XCD L2 and serialises
-// across workgroups, or write-through stores plus an arrival atomic per
-// workgroup, whose round trips and same-address serialisation cost more than
-// the second launch.)
+// scores (K Q^T) and the output (P V) run on the matrix cores, the softmax in
+// fp32 (scores scaled by log2(e)/sqrt(D), exp2); the chunk's unnormalised
+// output, maximum and sum go to a workspace and are merged over the chunks.
+// When Hkv is a multiple of 8 the merge happens in the same launch: all
+// chunks of one KV head run on one XCD (workgroups are dispatched to the 8
+// XCDs round-robin), so their partials meet in that XCD's L2, and the last
+// workgroup of the head to count itself in (an atomic in that L2) merges them.
+// A merge across XCDs in one launch was measured slower than a second launch:
+// it needs an agent-scope release (a write-back of the whole per-XCD L2,
+// serialised across workgroups) or write-through stores and device-scope
+// atomics. Other Hkv use a second small kernel for the merge.
 // RoPE for q and the new k is applied on load (two-halves rotation, row `pos`
 // of an fp32 [cos, sin] interleaved table, result rounded to bf16 as the RoPE
 // operator does), and the new k/v are written into the caches at `pos` by the
@@ -39,19 +42,29 @@ struct DecodeArgs {
   uint16_t* v_cache;      // (Hkv, max_len, D)
   const float* angles;    // (angle_rows, D) [cos0, sin0, cos1, sin1, ...]
   uint16_t* out;          // (H, D)
-  float* part;            // (Hkv, nsplit, G*D + 2G) partials
+  float* part;            // per KV head (head_stride floats): nsplit partials of part_stride<G>() floats
+  unsigned* ctr;          // per KV head (kCtrStride words): arrival counter of the one-launch path
+  long long head_stride;  // floats between the partial regions of consecutive KV heads
   const int* pos_dev;     // optional device-resident position (overrides pos)
   int pos;
   int max_len;
   int angle_rows;
-  int nsplit;             // gridDim.x
+  int nsplit;             // chunks per KV head
   float scale_log2;       // log2(e) * scale
 };
 
+// One chunk's partial: G x 64 unnormalised outputs, then G maxima, then G
+// sums, padded to a whole number of 16-byte quads.
 template <int G>
 constexpr int part_stride() {
-  return G * kD + 2 * G;
+  return (G * kD + 2 * G + 3) / 4 * 4;
 }
+
+// Workgroups are dispatched to the XCDs round-robin, so workgroups whose
+// linear ids agree mod 8 run on one XCD and share its L2. The one-launch path
+// gives each KV head such a class of ids (n_kv_heads a multiple of 8).
+constexpr int kXcds = 8;
+constexpr int kCtrStride = 32;  // counter words per KV head: one 128-byte line each
 
 // Loads of one 16-byte chunk as 8 floats.
 __device__ __forceinline__ void unpack8(const uint4 v, float* f) {
@@ -79,84 +92,137 @@ __device__ __forceinline__ void rope_chunk(const uint4 own, const uint4 pair, co
   }
 }
 
-// Lanes l and l ^ 32 of a and b summed in one exchange (v_permlane32_swap_b32
-// swaps the upper 32 lanes of its first operand with the lower 32 of its
-// second): lanes 0..31 return a[l] + a[l ^ 32], lanes 32..63 b[l] + b[l ^ 32].
-// Inline assembly: this compiler's builtins for the permlane swaps return the
-// first result in place of the second (seen in the generated code). The s_nop
-// covers the VALU-write to permlane-read hazard.
-__device__ __forceinline__ float fold32(float a, float b) {
-  unsigned x = __builtin_bit_cast(unsigned, a), y = __builtin_bit_cast(unsigned, b);
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+// Cross-lane exchanges by v_permlane32_swap_b32 / v_permlane16_swap_b32 with
+// both operands holding a: afterwards x[l] = a[l % 32], y[l] = a[l % 32 + 32]
+// (split32), or x[l], y[l] = a of the even and odd 16-lane row of l's pair
+// (split16), so that op(x, y) = op(a[l], a[l ^ 32]) (resp. a[l ^ 16]) on
+// every lane. Inline assembly: this compiler's builtins for the permlane swaps
+// return the first result in place of the second (seen in the generated code).
+// The s_nop covers the VALU-write to permlane-read hazard.
+__device__ __forceinline__ void split32(float a, float& x, float& y) {
+  unsigned u = __builtin_bit_cast(unsigned, a), v = u;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(v));
+  x = __builtin_bit_cast(float, u);
+  y = __builtin_bit_cast(float, v);
 }
-
-// The same over lanes l and l ^ 16 (v_permlane16_swap_b32 swaps the odd
-// 16-lane rows of its first operand with the even rows of its second): rows 0
-// and 2 return a[l] + a[l ^ 16], rows 1 and 3 b[l] + b[l ^ 16].
-__device__ __forceinline__ float fold16(float a, float b) {
-  unsigned x = __builtin_bit_cast(unsigned, a), y = __builtin_bit_cast(unsigned, b);
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
-  return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+__device__ __forceinline__ void split16(float a, float& x, float& y) {
+  unsigned u = __builtin_bit_cast(unsigned, a), v = u;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(u), "+v"(v));
+  x = __builtin_bit_cast(float, u);
+  y = __builtin_bit_cast(float, v);
+}
+// max / sum over lanes {l, l ^ 16, l ^ 32, l ^ 48}
+__device__ __forceinline__ float max_over_rows(float a) {
+  float x, y;
+  split32(a, x, y);
+  a = fmaxf(x, y);
+  split16(a, x, y);
+  return fmaxf(x, y);
+}
+__device__ __forceinline__ float sum_over_rows(float a) {
+  float x, y;
+  split32(a, x, y);
+  a = x + y;
+  split16(a, x, y);
+  return x + y;
 }
 
 // 2^x by v_exp_f32 alone, for x <= 0 (softmax weights): results below 2^-126
 // flush to zero, which the weights tolerate; elsewhere exp2f's value.
 __device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// One decode step of KV head j (blockIdx.y) for its G query heads; workgroup
-// s (blockIdx.x) owns cache positions [64 s, 64 s + 64).
+typedef __bf16 dec_bf16x8 __attribute__((ext_vector_type(8)));
+typedef short dec_i16x4 __attribute__((ext_vector_type(4)));
+typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
+
+// Slot of 16-byte chunk c of V row R (0..15) in a wave's LDS block: rows of
+// one parity in a 32-lane pass of the transposed read (R, R + 2, R + 4, R + 6)
+// land on disjoint bank groups. An involution in c.
+__device__ __forceinline__ int dec_v_slot(int R, int c) { return c ^ (((R >> 1) & 3) << 1); }
+
+// One decode step of KV head j for its G query heads; workgroup s owns cache
+// positions [64 s, 64 s + 64), wave w of it positions 64 s + 16 w + [0, 16).
 //
-// Wave w of the workgroup takes positions 64 s + 16 w + [0, 16): lane
-// (r = lane / 8, c = lane % 8) holds rows r and r + 8 of them, dims 8c..8c+7.
-// Every global load (K/V rows, q and the table row, the owner's new k/v) is
-// issued as soon as `pos` is known. q is rotated once per workgroup (one
-// element per thread) into LDS as bf16. Scores are bf16 dot products
-// (v_dot2_f32_bf16: exact products, fp32 sums) summed over the 8 lanes of a
-// row by DPP; the softmax statistics of the wave's 16 rows come from wave-wide
-// DPP reductions, and the wave's unnormalised output (G x 64 values, 8G per
-// lane) is summed over the 8 rows of lanes with two permlane folds and one
-// DPP step, which leave each lane 2G totals. The four waves meet once in LDS
-// to form the chunk's partial (output, maximum, sum), written to the
-// workspace for gqa_combine_kernel.
+// Per wave, on the matrix cores (v_mfma_f32_16x16x32_bf16 for the scores,
+// v_mfma_f32_16x16x16_bf16 for the output):
+//   S = K Q^T    A = the wave's 16 K rows straight from global memory (lane l:
+//                row l % 16, dims 8 (l / 16) + [0, 8) and 32 + the same),
+//                B = rotated q from LDS (column = head l % 16; heads >= G
+//                repeat a real head, and their rows of P and O are dropped);
+//                lane l then holds the scores of head l % 16 at positions
+//                4 (l / 16) + [0, 4).
+//   softmax      per head over the wave's 16 positions: the lane's own 4
+//                values and two permlane exchanges; fp32 weights in the log2
+//                domain.
+//   O = P V      A = P as bf16 pairs hi + lo (two MFMAs: the weights keep
+//                ~16 bits), B = V^T read from the wave's LDS block (filled by
+//                global_load_lds) with ds_read_b64_tr_b16; lane l (l / 16 <
+//                G / 4) ends with heads 4 (l / 16) + [0, 4) at dims 16 t + l % 16.
+// The new token's k (rotated) and v replace their row (and are appended to
+// the caches); rows past pos are masked (scores) and zeroed (V). The four
+// waves' (max, sum, output) meet once in LDS to form the chunk's partial.
+//
+// MERGE (the one-launch path): workgroup n takes KV head 8 (t / nsplit) + n % 8
+// and chunk t % nsplit, t = n / 8, so all chunks of a head run on one XCD.
+// After writing its partial a workgroup waits for its stores to reach that
+// XCD's L2 and counts itself in with an atomic there; the last of the head's
+// active chunks to arrive invalidates its CU's L1 and merges the head's
+// partials from the L2 (fused_merge), then returns the counter to zero. No
+// workgroup waits for another. Without MERGE the grid is (nsplit, Hkv) and
+// gqa_combine_kernel merges.
 template <int G>
+__device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid);
+
+template <int G, bool MERGE>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int NW = kDecThreads / kWave;
   constexpr int PS = part_stride<G>();
-  constexpr int NV = 8 * G;  // unnormalised output values per lane before the folds
   __shared__ __attribute__((aligned(16))) uint16_t q_s[G * D];  // rotated q, bf16
   __shared__ float wm_s[NW][G], wl_s[NW][G];
   __shared__ __attribute__((aligned(16))) float wo_s[NW][G * D];
+  __shared__ __attribute__((aligned(16))) unsigned char v_s[NW][16 * 128];  // each wave's 16 V rows
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
-  const int s = blockIdx.x, j = blockIdx.y;
+  int s, j;
+  if constexpr (MERGE) {
+    const int n = blockIdx.x, t = n / kXcds;
+    j = n % kXcds + kXcds * (t / a.nsplit);
+    s = t % a.nsplit;
+  } else {
+    s = blockIdx.x;
+    j = blockIdx.y;
+  }
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * kDecChunk;
   if (p0 >= L) return;
-  const int c = lane & 7, r = lane >> 3;
-  const bool lower = c < 4;
+  const int r = lane & 15, cq = lane >> 4;
   const int wrow0 = p0 + 16 * w;
-  const bool owner = pos >= wrow0 && pos < wrow0 + 16;
+  const bool owner_wave = pos >= wrow0 && pos < wrow0 + 16;
+  const bool owner = pos == wrow0 + r;  // the 4 lanes holding the new token's K row
+  const size_t hb = static_cast<size_t>(j) * a.max_len;
 
-  // cache rows: unconditional loads of a clamped row (a guarded load compiled
-  // to a branch that waited for its data); rows >= pos are replaced below
-  // (the new token) or masked (past it)
-  uint4 kraw[2], vraw[2];
+  // K rows (clamped: rows >= pos are replaced or masked below)
+  const int krow = min(wrow0 + r, a.max_len - 1);
+  uint4 k0 = ld_stream16(a.k_cache + (hb + krow) * D + cq * 8);
+  uint4 k1 = ld_stream16(a.k_cache + (hb + krow) * D + (cq + 4) * 8);
+  // V rows into the wave's LDS block: lane l of load u lands on row 8 u + l / 8, slot l % 8
+  unsigned char* vblk = v_s[w];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int p = min(wrow0 + r + 8 * h, a.max_len - 1);
-    const size_t off = (static_cast<size_t>(j) * a.max_len + p) * D + c * 8;
-    kraw[h] = ld_stream16(a.k_cache + off);
-    vraw[h] = ld_stream16(a.v_cache + off);
+  for (int u = 0; u < 2; ++u) {
+    const int R = 8 * u + (lane >> 3);
+    const int vrow = min(wrow0 + R, a.max_len - 1);
+    const uint16_t* src = a.v_cache + (hb + vrow) * D + dec_v_slot(R, lane & 7) * 8;
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src), reinterpret_cast<unsigned*>(vblk + u * 1024),
+                                     16, 0, 0);
   }
   const float* angrow = a.angles + static_cast<size_t>(pos) * D;
   float ang[16];
-  uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vn = kna;
-  if (owner) {  // the new token's table entries and k/v, in flight with the cache rows
-    const float4* ap = reinterpret_cast<const float4*>(angrow + (c & 3) * 16);
+  uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vna = kna, vnb = kna;
+  if (owner) {  // the new token's table entries (dims 8 cq + [0, 8)) and k/v chunks cq, cq + 4
+    const float4* ap = reinterpret_cast<const float4*>(angrow + cq * 16);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 t = ap[i];
@@ -165,9 +231,10 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
       ang[4 * i + 2] = t.z;
       ang[4 * i + 3] = t.w;
     }
-    kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + c * 8);
-    knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (c ^ 4) * 8);
-    vn = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + c * 8);
+    kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + cq * 8);
+    knb = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * D + (cq + 4) * 8);
+    vna = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + cq * 8);
+    vnb = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + (cq + 4) * 8);
   }
   const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
   for (int t = tid; t < G * D; t += kDecThreads) {
@@ -177,94 +244,104 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     q_s[t] = f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn);
   }
   __syncthreads();
-  uint4 qk[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) qk[g] = *reinterpret_cast<const uint4*>(&q_s[g * D + c * 8]);
+  const int hq = r & (G - 1);
+  const dec_bf16x8 qb0 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + cq * 8]);
+  const dec_bf16x8 qb1 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + (cq + 4) * 8]);
+
+  if (owner) {  // rotate the new k, append k/v to the caches
+    float lo[8], hi[8];
+    rope_chunk(kna, knb, ang, true, lo);
+    rope_chunk(knb, kna, ang, false, hi);
+    k0 = make_uint4(pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(lo[4], lo[5]),
+                    pack_bf16x2(lo[6], lo[7]));  // exact: bf16 values
+    k1 = make_uint4(pack_bf16x2(hi[0], hi[1]), pack_bf16x2(hi[2], hi[3]), pack_bf16x2(hi[4], hi[5]),
+                    pack_bf16x2(hi[6], hi[7]));
+    uint16_t* kp = a.k_cache + (hb + pos) * D;
+    uint16_t* vp = a.v_cache + (hb + pos) * D;
+    *reinterpret_cast<uint4*>(kp + cq * 8) = k0;
+    *reinterpret_cast<uint4*>(kp + (cq + 4) * 8) = k1;
+    *reinterpret_cast<uint4*>(vp + cq * 8) = vna;
+    *reinterpret_cast<uint4*>(vp + (cq + 4) * 8) = vnb;
+  }
 
   // One code path for waves whose 16 rows are all valid and none is the new
   // token (every wave but the last one or two), one with the masks and the
-  // owner's append.
-  const bool full = wrow0 + 16 <= L && !owner;  // wave-uniform
+  // owner's row.
+  const bool full = wrow0 + 16 <= L && !owner_wave;  // wave-uniform
   auto wave_body = [&](auto full_tag) {
     constexpr bool FULL = decltype(full_tag)::value;
-    // K rows as packed bf16, V rows as floats (zero past pos: 0 * stale data must not reach o)
-    uint32_t kw[2][4];
-    float vf[2][8];
-    bool valid[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int p = wrow0 + r + 8 * h;
-      valid[h] = FULL || p < L;
-      if (!FULL && p == pos) {  // the new token: rotate k, append k/v to the caches
-        float kr[8];
-        rope_chunk(kna, knb, ang, lower, kr);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) kw[h][e] = pack_bf16x2(kr[2 * e], kr[2 * e + 1]);  // exact: bf16 values
-        unpack8(vn, vf[h]);
-        const size_t off = (static_cast<size_t>(j) * a.max_len + pos) * D + c * 8;
-        *reinterpret_cast<uint4*>(a.k_cache + off) = make_uint4(kw[h][0], kw[h][1], kw[h][2], kw[h][3]);
-        *reinterpret_cast<uint4*>(a.v_cache + off) = vn;
-      } else {
-        kw[h][0] = kraw[h].x;
-        kw[h][1] = kraw[h].y;
-        kw[h][2] = kraw[h].z;
-        kw[h][3] = kraw[h].w;
-        unpack8(vraw[h], vf[h]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vf[h][e] = FULL || valid[h] ? vf[h][e] : 0.f;
-      }
-    }
+    dec_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dec_bf16x8, k0), qb0, sacc, 0, 0, 0);
+    sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dec_bf16x8, k1), qb1, sacc, 0, 0, 0);
 
-    // scores in the log2 domain; the 8 lanes of a row sum their partial dots
-    float sc[2][G];
+    // softmax of head r over positions wrow0 + 4 cq + i (log2 domain)
+    float sv[4];
+    bool valid[4];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int i = 0; i < 4; ++i) {
+      valid[i] = FULL || wrow0 + 4 * cq + i < L;
+      sv[i] = valid[i] ? sacc[i] * a.scale_log2 : -INFINITY;
+    }
+    const float m = max_over_rows(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));  // -inf only if all 16 rows are past pos
+    float e[4];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = dot2_bf16(qk[g].x, kw[h][0], 0.f);
-        d = dot2_bf16(qk[g].y, kw[h][1], d);
-        d = dot2_bf16(qk[g].z, kw[h][2], d);
-        d = dot2_bf16(qk[g].w, kw[h][3], d);
-        d = add_dpp<0xB1>(d);   // + lane ^ 1
-        d = add_dpp<0x4E>(d);   // + lane ^ 2
-        d = add_dpp<0x141>(d);  // + lane 7-i of the 8: full 8-lane sum
-        sc[h][g] = FULL || valid[h] ? d * a.scale_log2 : -INFINITY;
-      }
+    for (int i = 0; i < 4; ++i) e[i] = FULL || valid[i] ? exp2_weight(sv[i] - m) : 0.f;
+    const float lsum = sum_over_rows((e[0] + e[1]) + (e[2] + e[3]));
+    // P = hi + lo, both bf16
+    const uint32_t h01 = pack_bf16x2(e[0], e[1]), h23 = pack_bf16x2(e[2], e[3]);
+    const uint32_t l01 = pack_bf16x2(e[0] - lo_bf16(h01), e[1] - hi_bf16(h01));
+    const uint32_t l23 = pack_bf16x2(e[2] - lo_bf16(h23), e[3] - hi_bf16(h23));
+    const dec_i16x4 phi = __builtin_bit_cast(dec_i16x4, make_uint2(h01, h23));
+    const dec_i16x4 plo = __builtin_bit_cast(dec_i16x4, make_uint2(l01, l23));
 
-    // the wave's statistics and unnormalised output over its 16 rows
-    float ov[NV];
+    // V: wait for the LDS-direct rows; rows past pos become zeros (0 x stale
+    // data must not reach O), the new token's row takes v_new
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (!FULL) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m = wave_max(fmaxf(sc[0][g], sc[1][g]));  // -inf only when all 16 rows are past pos
-      const float e0 = FULL || valid[0] ? exp2_weight(sc[0][g] - m) : 0.f;
-      const float e1 = FULL || valid[1] ? exp2_weight(sc[1][g] - m) : 0.f;
-      const float l = wave_sum(c == 0 ? e0 + e1 : 0.f);
-      if (lane == 0) {
-        wm_s[w][g] = m;
-        wl_s[w][g] = l;
+      for (int u = 0; u < 2; ++u)
+        if (wrow0 + 8 * u + (lane >> 3) > pos)
+          *reinterpret_cast<uint4*>(vblk + u * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
+      if (owner) {
+        *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq) * 16) = vna;
+        *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq + 4) * 16) = vnb;
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ov[g * 8 + e] = fmaf(e0, vf[0][e], e1 * vf[1][e]);
     }
-    // sum over the 8 rows r (lane bits 3..5): value k pairs with k + NV/2 across
-    // lane bit 5, then with k + NV/4 across bit 4, then a DPP step over bit 3
-    float o2[NV / 2], o4[NV / 4];
+    // V^T operands: in each 16-lane group g lane 4 jj + qq addresses row 4 g + jj,
+    // dims 16 t + 4 qq .. + 3; lane i of the group then receives dim 16 t + i
+    // of rows 4 g + [0, 4)
+    const int tR = 4 * cq + (r >> 2);
+    const unsigned vb = static_cast<unsigned>(reinterpret_cast<uintptr_t>(vblk)) + tR * 128 + 8 * (lane & 1);
+    uint2 vt[4];
+    {
+      unsigned ad[4];
 #pragma unroll
-    for (int k = 0; k < NV / 2; ++k) o2[k] = fold32(ov[k], ov[k + NV / 2]);
-#pragma unroll
-    for (int k = 0; k < NV / 4; ++k) {
-      const float t = fold16(o2[k], o2[k + NV / 4]);
-      o4[k] = t + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, t), 0x128, 0xf,
-                                                                            0xf, false));  // row_ror:8 = lane ^ 8
+      for (int t = 0; t < 4; ++t) ad[t] = vb + dec_v_slot(tR, 2 * t + ((lane & 3) >> 1)) * 16;
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %5\n\t"
+          "ds_read_b64_tr_b16 %2, %6\n\tds_read_b64_tr_b16 %3, %7\n\t"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]), "=&v"(vt[3])
+          : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+          : "memory");
     }
-    // lane holds totals k = (lane bit 5) NV/2 + (lane bit 4) NV/4 + [0, NV/4): value k is (g = k / 8, dim 8c + k % 8)
-    if (((lane >> 3) & 1) == 0) {
-      const int k0 = (lane >> 5) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+    dec_f32x4 o[4];
 #pragma unroll
-      for (int k = 0; k < NV / 4; ++k) {
-        const int kk = k0 + k;
-        wo_s[w][(kk / 8) * D + c * 8 + kk % 8] = o4[k];
-      }
+    for (int t = 0; t < 4; ++t) {
+      const dec_i16x4 vv = __builtin_bit_cast(dec_i16x4, vt[t]);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(phi, vv, dec_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(plo, vv, o[t], 0, 0, 0);
+    }
+    if (lane < G) {
+      wm_s[w][lane] = m;
+      wl_s[w][lane] = lsum;
+    }
+    if (4 * cq < G) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * cq + i < G) wo_s[w][(4 * cq + i) * D + 16 * t + r] = o[t][i];
     }
   };
   if (full)
@@ -274,7 +351,7 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   __syncthreads();
 
   // the chunk's partial: the four waves merged
-  float* part = a.part + (static_cast<size_t>(j) * a.nsplit + s) * PS;
+  float* part = a.part + static_cast<size_t>(j) * a.head_stride + static_cast<size_t>(s) * PS;
   for (int t = tid; t < G * D; t += kDecThreads) {
     const int g = t / D;
     float M = wm_s[0][g];  // finite: position p0 < L is in wave 0
@@ -292,6 +369,103 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
       part[G * D + g] = M;
       part[G * D + G + g] = l;
     }
+  }
+  if constexpr (MERGE) {
+    __shared__ int last_s;
+    const int nact = (L + kDecChunk - 1) / kDecChunk;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have reached the L2
+    __syncthreads();
+    if (tid == 0) {
+      unsigned* c = a.ctr + static_cast<size_t>(j) * kCtrStride;
+      const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int last = old == static_cast<unsigned>(nact - 1);
+      if (last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      last_s = last;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    asm volatile("buffer_inv sc0" ::: "memory");  // no stale line of the head's partials in this CU's L1
+    fused_merge<G>(a, j, nact, tid);
+  }
+}
+
+// The merge of KV head j's nact chunk partials by one 256-thread workgroup:
+// thread -> 4 consecutive output values (quad qd of the G x 64 outputs) and
+// slice q of the chunks (q, q + NQ, ...), folded with a running maximum in
+// batches of 16 chunks whose loads are all in flight together; the NQ slices
+// then meet in LDS.
+template <int G>
+__device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid) {
+  constexpr int D = kD;
+  constexpr int PS = part_stride<G>();
+  constexpr int NQD = G * D / 4;           // quads per chunk
+  constexpr int NQ = kDecThreads / NQD;    // chunk slices
+  constexpr int B = 16;                    // chunks per batch per thread
+  __shared__ float mm_s[kDecThreads], ll_s[kDecThreads];
+  __shared__ float4 oo_s[kDecThreads];
+  const int qd = tid % NQD, q = tid / NQD, g = qd / (D / 4);
+  const float* base = a.part + static_cast<size_t>(j) * a.head_stride;
+  float M = -INFINITY, Ls = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k0 = q; k0 < nact; k0 += NQ * B) {
+    float mb[B], lb[B];
+    float4 ob[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {  // clamped chunk index: every load lands in the head's region
+      const float* pk = base + static_cast<size_t>(min(k0 + b * NQ, nact - 1)) * PS;
+      ob[b] = *reinterpret_cast<const float4*>(pk + 4 * qd);
+      mb[b] = pk[G * D + g];
+      lb[b] = pk[G * D + G + g];
+    }
+    float bm = M;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool live = k0 + b * NQ < nact;
+      mb[b] = live ? mb[b] : -INFINITY;
+      lb[b] = live ? lb[b] : 0.f;
+      bm = fmaxf(bm, mb[b]);  // finite: chunk k0 < nact is live
+    }
+    const float keep = exp2f(M - bm);  // 0 on the first batch
+    acc.x *= keep;
+    acc.y *= keep;
+    acc.z *= keep;
+    acc.w *= keep;
+    Ls *= keep;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const float wgt = exp2f(mb[b] - bm);  // 0 for the chunks past nact
+      const bool live = k0 + b * NQ < nact;
+      acc.x = fmaf(wgt, live ? ob[b].x : 0.f, acc.x);
+      acc.y = fmaf(wgt, live ? ob[b].y : 0.f, acc.y);
+      acc.z = fmaf(wgt, live ? ob[b].z : 0.f, acc.z);
+      acc.w = fmaf(wgt, live ? ob[b].w : 0.f, acc.w);
+      Ls = fmaf(wgt, lb[b], Ls);
+    }
+    M = bm;
+  }
+  mm_s[tid] = M;
+  ll_s[tid] = Ls;
+  oo_s[tid] = acc;
+  __syncthreads();
+  if (q == 0) {
+    float Mx = M;  // slice 0 holds chunk 0
+#pragma unroll
+    for (int qq = 1; qq < NQ; ++qq) Mx = fmaxf(Mx, mm_s[qq * NQD + qd]);
+    float lt = 0.f;
+    float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq) {
+      const float wgt = exp2f(mm_s[qq * NQD + qd] - Mx);  // 0 for an empty slice
+      const float4 o = oo_s[qq * NQD + qd];
+      lt = fmaf(wgt, ll_s[qq * NQD + qd], lt);
+      ot.x = fmaf(wgt, o.x, ot.x);
+      ot.y = fmaf(wgt, o.y, ot.y);
+      ot.z = fmaf(wgt, o.z, ot.z);
+      ot.w = fmaf(wgt, o.w, ot.w);
+    }
+    const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(ot.x / lt)) | (static_cast<uint32_t>(f32_to_bf16(ot.y / lt)) << 16);
+    const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(ot.z / lt)) | (static_cast<uint32_t>(f32_to_bf16(ot.w / lt)) << 16);
+    *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(j) * G * D + 4 * qd) = make_uint2(lo, hi);
   }
 }
 
@@ -312,7 +486,7 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
   __shared__ float m_s[kMergeThreads], l_s[kMergeThreads], o_s[kMergeThreads];
   const int tid = threadIdx.x, d = tid % D, q = tid / D;
   const int h = blockIdx.x, j = h / G, g = h % G;
-  const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
+  const float* base = a.part + static_cast<size_t>(j) * a.head_stride;
   // The first B chunks of this slice are loaded before the position is known
   // (any chunk < nsplit is inside the workspace); chunks past the active count
   // are dropped by selects below, so stale workspace values never mix in.
@@ -380,51 +554,10 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
   }
 }
 
-// Merge of the chunk partials with one wave per query head (Hkv * G
-// workgroups of 64 threads): lane i holds the statistics (maximum, sum) of
-// chunks i, i + 64, ..., lane d accumulates output dim d, and each chunk's
-// weight reaches every lane by readlane. The loads of the first 64 chunks are
-// issued before the position is read, so a context of up to 4096 positions
-// costs one memory round trip. Chunks past the active count are dropped by
-// selects (their workspace may hold anything).
-template <int G>
-__global__ __launch_bounds__(kWave) void gqa_merge_kernel(DecodeArgs a) {
-  constexpr int D = kD;
-  constexpr int PS = part_stride<G>();
-  const int lane = threadIdx.x;
-  const int h = blockIdx.x, j = h / G, g = h % G;
-  const float* base = a.part + static_cast<size_t>(j) * a.nsplit * PS;
-  const float* pl = base + static_cast<size_t>(min(lane, a.nsplit - 1)) * PS;
-  float mb = pl[G * D + g], lb = pl[G * D + G + g];
-  float ob[kWave];
-#pragma unroll
-  for (int u = 0; u < kWave; ++u) ob[u] = base[static_cast<size_t>(min(u, a.nsplit - 1)) * PS + g * D + lane];
-  const int pos = a.pos_dev ? *a.pos_dev : a.pos;
-  if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;
-  const int nact = (pos + kDecChunk) / kDecChunk;
-  float M = lane < nact ? mb : -INFINITY;
-  for (int i = lane + kWave; i < nact; i += kWave) M = fmaxf(M, base[static_cast<size_t>(i) * PS + G * D + g]);
-  M = wave_max(M);  // finite: chunk 0 is active
-  float acc = 0.f, Ls = 0.f;
-  for (int b0 = 0; b0 < nact; b0 += kWave) {
-    if (b0 > 0) {  // contexts past 64 chunks: the next 64
-      const float* pb = base + static_cast<size_t>(min(b0 + lane, nact - 1)) * PS;
-      mb = pb[G * D + g];
-      lb = pb[G * D + G + g];
-#pragma unroll
-      for (int u = 0; u < kWave; ++u) ob[u] = base[static_cast<size_t>(min(b0 + u, nact - 1)) * PS + g * D + lane];
-    }
-    const bool live = b0 + lane < nact;
-    const float wgt = live ? exp2f(mb - M) : 0.f;
-    Ls = fmaf(wgt, live ? lb : 0.f, Ls);
-#pragma unroll
-    for (int u = 0; u < kWave; ++u) {
-      const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
-      acc = fmaf(wu, b0 + u < nact ? ob[u] : 0.f, acc);
-    }
-  }
-  Ls = wave_sum(Ls);
-  a.out[static_cast<size_t>(h) * D + lane] = f32_to_bf16(acc / Ls);
+// Zeroes the arrival counters of the one-launch path (one word per KV head),
+// for callers whose workspace carries no state between calls.
+__global__ __launch_bounds__(kWave) void gqa_clear_counters_kernel(unsigned* ctr, int n_kv_heads) {
+  for (int j = threadIdx.x; j < n_kv_heads; j += kWave) ctr[static_cast<size_t>(j) * kCtrStride] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -789,28 +922,45 @@ using namespace iron;
 
 static int decode_nsplit(int max_len) { return (max_len + kDecChunk - 1) / kDecChunk; }
 
+static int decode_part_stride(int G) {
+  switch (G) {
+    case 1: return part_stride<1>();
+    case 2: return part_stride<2>();
+    case 4: return part_stride<4>();
+    default: return part_stride<8>();
+  }
+}
+
+// Workspace layout: the arrival counters (one 128-byte line per KV head,
+// rounded up to 256 bytes), then per KV head its nsplit chunk partials,
+// each head's region rounded up to 256 bytes.
+static long long decode_ctr_bytes(int n_kv_heads) { return (static_cast<long long>(n_kv_heads) * kCtrStride * 4 + 255) / 256 * 256; }
+static long long decode_head_stride(int G, int max_len) {
+  return (static_cast<long long>(decode_nsplit(max_len)) * decode_part_stride(G) + 63) / 64 * 64;
+}
+
 extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len) {
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim != kD || max_len <= 0) return -1;
   const int G = n_heads / n_kv_heads;
-  const long long part = static_cast<long long>(n_kv_heads) * decode_nsplit(max_len) * (G * kD + 2 * G) * 4;
-  return 256 + part;  // 256 reserved bytes, then partials
+  if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
+  return decode_ctr_bytes(n_kv_heads) + static_cast<long long>(n_kv_heads) * decode_head_stride(G, max_len) * 4;
 }
 
-// Checks and launches of one GQA decode step with its partials in `workspace`
-// (iron_gqa_decode_workspace_bytes() of the shape, 256-byte aligned); shared
-// by the entry point that takes a workspace and the one that uses the
-// library's own scratch array.
+// Checks and launches of one GQA decode step with its counters and partials
+// in `workspace` (iron_gqa_decode_workspace_bytes() of the shape, 256-byte
+// aligned); shared by the entry point that takes a workspace (counters kept
+// at zero between calls) and the one that uses the library's own scratch
+// array (clear_counters: zeroed before each call by a small kernel).
 static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
                              void* v_cache, const float* angles, int angle_rows, void* out, void* workspace,
                              int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
-                             float scale, void* stream) {
+                             float scale, void* stream, bool clear_counters) {
   IRON_REQUIRE(q && k_new && v_new && k_cache && v_cache && angles && out && workspace, "%s: null pointer", who);
   IRON_REQUIRE(head_dim == kD, "%s: head_dim=%d (only 64 is supported)", who, head_dim);
   IRON_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
                "%s: n_heads=%d must be a multiple of n_kv_heads=%d", who, n_heads, n_kv_heads);
   const int G = n_heads / n_kv_heads;
   IRON_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "%s: group size %d not in {1,2,4,8}", who, G);
-  IRON_REQUIRE(n_kv_heads * 4 <= 256, "%s: at most 64 KV heads", who);
   IRON_REQUIRE(max_len > 0 && angle_rows > 0, "%s: max_len and angle_rows must be positive", who);
   IRON_REQUIRE(pos_dev || (pos >= 0 && pos < max_len && pos < angle_rows),
                "%s: pos=%d outside the cache (max_len=%d) or angle table (%d rows)", who, pos, max_len, angle_rows);
@@ -826,31 +976,44 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.v_cache = static_cast<uint16_t*>(v_cache);
   a.angles = angles;
   a.out = static_cast<uint16_t*>(out);
-  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+  a.ctr = static_cast<unsigned*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + decode_ctr_bytes(n_kv_heads));
+  a.head_stride = decode_head_stride(G, max_len);
   a.pos_dev = pos_dev;
   a.pos = pos;
   a.max_len = max_len;
   a.angle_rows = angle_rows;
   a.nsplit = decode_nsplit(max_len);
   a.scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid(a.nsplit, n_kv_heads), block(kDecThreads);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 cgrid(n_kv_heads * G), cblock(kMergeThreads);
+  const dim3 block(kDecThreads);
+  if (n_kv_heads % kXcds == 0) {  // one launch: each KV head's chunks on one XCD, merged by the last to finish
+    if (clear_counters) IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
+    const dim3 grid(a.nsplit * n_kv_heads);
+    switch (G) {
+      case 1: IRON_LAUNCH((gqa_decode_kernel<1, true>), grid, block, 0, s, a); break;
+      case 2: IRON_LAUNCH((gqa_decode_kernel<2, true>), grid, block, 0, s, a); break;
+      case 4: IRON_LAUNCH((gqa_decode_kernel<4, true>), grid, block, 0, s, a); break;
+      default: IRON_LAUNCH((gqa_decode_kernel<8, true>), grid, block, 0, s, a); break;
+    }
+    return check_launch(who);
+  }
+  const dim3 grid(a.nsplit, n_kv_heads), cgrid(n_kv_heads * G), cblock(kMergeThreads);
   switch (G) {
     case 1:
-      IRON_LAUNCH((gqa_decode_kernel<1>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_decode_kernel<1, false>), grid, block, 0, s, a);
       IRON_LAUNCH((gqa_combine_kernel<1>), cgrid, cblock, 0, s, a);
       break;
     case 2:
-      IRON_LAUNCH((gqa_decode_kernel<2>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_decode_kernel<2, false>), grid, block, 0, s, a);
       IRON_LAUNCH((gqa_combine_kernel<2>), cgrid, cblock, 0, s, a);
       break;
     case 4:
-      IRON_LAUNCH((gqa_decode_kernel<4>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_decode_kernel<4, false>), grid, block, 0, s, a);
       IRON_LAUNCH((gqa_combine_kernel<4>), cgrid, cblock, 0, s, a);
       break;
     default:
-      IRON_LAUNCH((gqa_decode_kernel<8>), grid, block, 0, s, a);
+      IRON_LAUNCH((gqa_decode_kernel<8, false>), grid, block, 0, s, a);
       IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, cblock, 0, s, a);
       break;
   }
@@ -862,7 +1025,7 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
                                int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
                                void* stream) {
   return gqa_decode_launch("iron_gqa_decode", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, workspace,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false);
 }
 
 // The workspace of iron_gqa_decode_noalloc: a file-scope device array, one
@@ -919,7 +1082,7 @@ extern "C" int iron_gqa_decode_noalloc(const void* q, const void* k_new, const v
   void* ws = decode_scratch_ptr("iron_gqa_decode_noalloc");
   if (!ws) return IRON_EINVAL;
   return gqa_decode_launch("iron_gqa_decode_noalloc", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, ws,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, true);
 }
 
 extern "C" int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads,

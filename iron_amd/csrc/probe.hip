@@ -46,6 +46,14 @@ __global__ __launch_bounds__(kProbeThreads) void stream_read_kernel(const uint4*
   }
 }
 
+// The XCD each workgroup runs on (hardware register XCC_ID, low 4 bits),
+// one word per workgroup.
+__global__ __launch_bounds__(kProbeThreads) void xcc_id_kernel(int* __restrict__ ids) {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  if (threadIdx.x == 0) ids[blockIdx.x] = static_cast<int>(x & 15u);
+}
+
 typedef __bf16 probe_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float probe_f32x16 __attribute__((ext_vector_type(16)));
 
@@ -158,4 +166,13 @@ extern "C" int iron_probe_read(const void* src, long long nbytes, void* sink, lo
     default: IRON_LAUNCH(stream_read_kernel<8>, grid, block, 0, s, s4, n16, out); break;
   }
   return check_launch("probe_read");
+}
+
+extern "C" int iron_probe_xcc_ids(int workgroups, void* ids, void* stream) {
+  IRON_REQUIRE(ids, "iron_probe_xcc_ids: null pointer");
+  IRON_REQUIRE(workgroups > 0 && workgroups <= (1 << 20), "iron_probe_xcc_ids: workgroups=%d outside [1, 2^20]",
+               workgroups);
+  IRON_LAUNCH(xcc_id_kernel, dim3(workgroups), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream),
+              static_cast<int*>(ids));
+  return check_launch("probe_xcc_ids");
 }

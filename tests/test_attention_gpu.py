@@ -18,24 +18,35 @@ pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
 
 
-def _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, pos_tensor=False):
+def _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, pos_tensor=False, op=None, fill=0.0):
+    """One decode step through the GQADecode operator. The cache rows before pos
+    hold kc/vc; the rows from pos on hold `fill` (stale data the step must not
+    read: only row pos is written, the rest stays masked)."""
     from iron_amd.operators import GQADecode
 
     H, Hkv = q.shape[0], kn.shape[0]
-    op = GQADecode(num_heads=H, num_kv_heads=Hkv, head_dim=64, max_len=max_len, angle_rows=angles.shape[0])
-    kcd = torch.zeros(Hkv, max_len, 64, dtype=BF16, device=gpu)
-    vcd = torch.zeros(Hkv, max_len, 64, dtype=BF16, device=gpu)
+    if op is None:
+        op = GQADecode(num_heads=H, num_kv_heads=Hkv, head_dim=64, max_len=max_len, angle_rows=angles.shape[0])
+    kcd = torch.full((Hkv, max_len, 64), fill, dtype=BF16, device=gpu)
+    vcd = torch.full((Hkv, max_len, 64), fill, dtype=BF16, device=gpu)
     kcd[:, :pos] = kc[:, :pos].to(gpu)
     vcd[:, :pos] = vc[:, :pos].to(gpu)
     out = torch.empty(H, 64, dtype=BF16, device=gpu)
     if pos_tensor:
         op.position_tensor = torch.tensor([pos], dtype=torch.int32, device=gpu)
     else:
+        op.position_tensor = None
         op.set_position(pos)
     fn = op.get_callable()
     fn(q.to(gpu), kn.to(gpu), vn.to(gpu), kcd, vcd, angles.to(gpu), out)
     torch.cuda.synchronize()
     return out.cpu(), kcd.cpu(), vcd.cpu(), op
+
+
+def _counters(op, gpu):
+    """The workspace's arrival counters (one 128-byte line per KV head)."""
+    ws = op.workspace(torch.device(gpu))
+    return ws[: 128 * op.num_kv_heads].view(torch.int32).view(op.num_kv_heads, 32)[:, 0].cpu()
 
 
 def test_config3_gqa_decode(gpu):
@@ -48,7 +59,7 @@ def test_config3_gqa_decode(gpu):
     assert torch.equal(kcd[:, pos], kref[:, pos]) and torch.equal(vcd[:, pos], vref[:, pos])
 
 
-@pytest.mark.parametrize("pos", [0, 1, 63, 64, 65, 127, 1000, 4095])
+@pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 127, 1000, 4095])
 @pytest.mark.parametrize("use_tensor", [False, True])
 def test_gqa_decode_positions(gpu, pos, use_tensor):
     max_len = 4096
@@ -61,26 +72,70 @@ def test_gqa_decode_positions(gpu, pos, use_tensor):
     assert torch.equal(kcd[:, pos], kref[:, pos])
 
 
-@pytest.mark.parametrize("H,Hkv", [(32, 32), (32, 16), (16, 2)])
+# n_kv_heads a multiple of 8: one launch (merge in the last workgroup of each
+# KV head); otherwise partials + merge kernel. Every group size on both.
+@pytest.mark.parametrize("H,Hkv", [(32, 32), (32, 16), (64, 8), (8, 8), (16, 2), (8, 2), (8, 4), (4, 4), (24, 24)])
 def test_gqa_decode_group_sizes(gpu, H, Hkv):
     q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, L=300, seed=3)
-    ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
-    out, _, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
+    ref, kref, vref = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    out, kcd, vcd, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
     max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
-    assert max_abs <= 2e-2 and rel_l2 <= 1e-2
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+    assert torch.equal(kcd[:, pos], kref[:, pos]) and torch.equal(vcd[:, pos], vref[:, pos])
 
 
-def test_gqa_decode_workspace_reuse(gpu):
-    """The ticket counters reset themselves: repeated calls on one workspace stay correct."""
-    q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(L=512, seed=11)
+@pytest.mark.parametrize("Hkv", [8, 2])
+@pytest.mark.parametrize("fill", [float("nan"), float("inf")])
+@pytest.mark.parametrize("pos", [0, 70, 383])
+def test_gqa_decode_ignores_stale_rows(gpu, Hkv, fill, pos):
+    """Cache rows past pos (in the last chunk and the whole chunks after it)
+    hold NaN or inf: neither their scores nor their values may reach the
+    output, on both launch paths."""
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(n_heads=4 * Hkv, n_kv=Hkv, L=512, seed=pos + 5)
+    angles = ops.rope_angles_table(64, 512)
     ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
-    out, _, _, op = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
-    ws = op.workspace(torch.device(gpu))
-    assert int(ws[:256].view(torch.int32).abs().sum()) == 0
-    for _ in range(3):
-        out2, _, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512)
-        assert torch.equal(out2, out)
-    assert ops.max_abs_rel_l2(out, ref)[0] <= 2e-2
+    out, _, _, _ = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len=512, fill=fill)
+    assert torch.isfinite(out.float()).all()
+    max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+
+
+@pytest.mark.parametrize("Hkv", [8, 16, 2])
+def test_gqa_decode_workspace_reuse(gpu, Hkv):
+    """One operator and workspace over calls at changing positions (so the
+    number of active chunks changes from call to call): every call matches the
+    oracle, repeats are bitwise equal, and the arrival counters are back at
+    zero after each call."""
+    max_len = 640
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(n_heads=4 * Hkv, n_kv=Hkv, L=max_len, seed=11)
+    angles = ops.rope_angles_table(64, max_len)
+    op = None
+    first = {}
+    for pos in [500, 100, 300, 37, 639, 0, 500, 100]:
+        out, _, _, op = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, op=op, pos_tensor=pos % 2 == 1)
+        ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+        max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+        assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (pos, max_abs, rel_l2)
+        if pos in first:
+            assert torch.equal(out, first[pos]), pos
+        first[pos] = out
+        assert int(_counters(op, gpu).abs().sum()) == 0, pos
+
+
+@pytest.mark.parametrize("workgroups", [8, 256, 576, 1000, 4104])
+def test_xcd_dispatch_is_round_robin(gpu, workgroups):
+    """The one-launch decode needs workgroups whose linear ids agree mod 8 to
+    share an XCD (and so an L2). Read each workgroup's XCC_ID and check it."""
+    from iron_amd import _lib
+
+    ids = torch.full((workgroups,), -1, dtype=torch.int32, device=gpu)
+    _lib.call("iron_probe_xcc_ids", workgroups, ids.data_ptr(), _lib.stream_handle(gpu))
+    torch.cuda.synchronize()
+    h = ids.cpu()
+    assert int(h.min()) >= 0
+    n = torch.arange(workgroups)
+    assert torch.equal(h, h[n % 8]), h[:16].tolist()
+    assert len(set(h[:8].tolist())) == 8  # eight XCDs, one class each
 
 
 @pytest.mark.parametrize(
