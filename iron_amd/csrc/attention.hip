@@ -204,20 +204,10 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   const bool owner = pos == wrow0 + r;  // the 4 lanes holding the new token's K row
   const size_t hb = static_cast<size_t>(j) * a.max_len;
 
-  // K rows (clamped: rows >= pos are replaced or masked below)
-  const int krow = min(wrow0 + r, a.max_len - 1);
-  uint4 k0 = ld_stream16(a.k_cache + (hb + krow) * D + cq * 8);
-  uint4 k1 = ld_stream16(a.k_cache + (hb + krow) * D + (cq + 4) * 8);
-  // V rows into the wave's LDS block: lane l of load u lands on row 8 u + l / 8, slot l % 8
-  unsigned char* vblk = v_s[w];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int R = 8 * u + (lane >> 3);
-    const int vrow = min(wrow0 + R, a.max_len - 1);
-    const uint16_t* src = a.v_cache + (hb + vrow) * D + dec_v_slot(R, lane & 7) * 8;
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src), reinterpret_cast<unsigned*>(vblk + u * 1024),
-                                     16, 0, 0);
-  }
+  // Loads, oldest first: the new token's table entries and k/v (owner lanes),
+  // then q and its table row, then the K rows, then the V rows. q is rotated
+  // while K and V are still in flight (the waits below count only what the
+  // rotation needs), and the scores wait for K alone.
   const float* angrow = a.angles + static_cast<size_t>(pos) * D;
   float ang[16];
   uint4 kna = make_uint4(0, 0, 0, 0), knb = kna, vna = kna, vnb = kna;
@@ -236,14 +226,43 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     vna = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + cq * 8);
     vnb = *reinterpret_cast<const uint4*>(a.v_new + static_cast<size_t>(j) * D + (cq + 4) * 8);
   }
+  constexpr int QN = (G * D + kDecThreads - 1) / kDecThreads;  // q elements per thread
   const uint16_t* qh = a.q + static_cast<size_t>(j) * G * D;
-  for (int t = tid; t < G * D; t += kDecThreads) {
-    const int d = t % D, i = d & 31;
-    const float x = bf16_to_f32(qh[t]), xp = bf16_to_f32(qh[t ^ 32]);
-    const float cs = angrow[2 * i], sn = angrow[2 * i + 1];
-    q_s[t] = f32_to_bf16(d < 32 ? x * cs - xp * sn : x * cs + xp * sn);
+  uint16_t qx[QN], qp[QN];
+  float2 qa[QN];
+#pragma unroll
+  for (int e = 0; e < QN; ++e) {
+    const int t = min(tid + kDecThreads * e, G * D - 1), i = (t % D) & 31;
+    qx[e] = qh[t];
+    qp[e] = qh[t ^ 32];
+    qa[e] = *reinterpret_cast<const float2*>(angrow + 2 * i);
   }
-  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);  // keep the q loads ahead of the K/V loads
+  // K rows (clamped: rows >= pos are replaced or masked below)
+  const int krow = min(wrow0 + r, a.max_len - 1);
+  uint4 k0 = ld_stream16(a.k_cache + (hb + krow) * D + cq * 8);
+  uint4 k1 = ld_stream16(a.k_cache + (hb + krow) * D + (cq + 4) * 8);
+  // V rows: lane l of load u holds row 8 u + l / 8, 16-byte chunk dec_v_slot(row, l % 8),
+  // stored below into slot l % 8 of the wave's LDS block
+  unsigned char* vblk = v_s[w];
+  uint4 vraw[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int R = 8 * u + (lane >> 3);
+    const int vrow = min(wrow0 + R, a.max_len - 1);
+    vraw[u] = ld_stream16(a.v_cache + (hb + vrow) * D + dec_v_slot(R, lane & 7) * 8);
+  }
+#pragma unroll
+  for (int e = 0; e < QN; ++e) {
+    const int t = tid + kDecThreads * e;
+    if (t < G * D) {
+      const float x = bf16_to_f32(qx[e]), xp = bf16_to_f32(qp[e]);
+      q_s[t] = f32_to_bf16((t % D) < 32 ? x * qa[e].x - xp * qa[e].y : x * qa[e].x + xp * qa[e].y);
+    }
+  }
+  // barrier without a wait for the K/V loads in flight (__syncthreads would
+  // wait for all of them); the memory clobber keeps the q_s accesses on their sides
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   const int hq = r & (G - 1);
   const dec_bf16x8 qb0 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + cq * 8]);
   const dec_bf16x8 qb1 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + (cq + 4) * 8]);
@@ -294,18 +313,16 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     const dec_i16x4 phi = __builtin_bit_cast(dec_i16x4, make_uint2(h01, h23));
     const dec_i16x4 plo = __builtin_bit_cast(dec_i16x4, make_uint2(l01, l23));
 
-    // V: wait for the LDS-direct rows; rows past pos become zeros (0 x stale
+    // V rows into the wave's LDS block; rows past pos become zeros (0 x stale
     // data must not reach O), the new token's row takes v_new
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (!FULL) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        if (wrow0 + 8 * u + (lane >> 3) > pos)
-          *reinterpret_cast<uint4*>(vblk + u * 1024 + lane * 16) = make_uint4(0, 0, 0, 0);
-      if (owner) {
-        *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq) * 16) = vna;
-        *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq + 4) * 16) = vnb;
-      }
+    for (int u = 0; u < 2; ++u) {
+      const bool stale = !FULL && wrow0 + 8 * u + (lane >> 3) > pos;
+      *reinterpret_cast<uint4*>(vblk + u * 1024 + lane * 16) = stale ? make_uint4(0, 0, 0, 0) : vraw[u];
+    }
+    if (!FULL && owner) {
+      *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq) * 16) = vna;
+      *reinterpret_cast<uint4*>(vblk + r * 128 + dec_v_slot(r, cq + 4) * 16) = vnb;
     }
     // V^T operands: in each 16-lane group g lane 4 jj + qq addresses row 4 g + jj,
     // dims 16 t + 4 qq .. + 3; lane i of the group then receives dim 16 t + i
@@ -389,82 +406,138 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   }
 }
 
-// The merge of KV head j's nact chunk partials by one 256-thread workgroup:
-// thread -> 4 consecutive output values (quad qd of the G x 64 outputs) and
-// slice q of the chunks (q, q + NQ, ...), folded with a running maximum in
-// batches of 16 chunks whose loads are all in flight together; the NQ slices
-// then meet in LDS.
+// The merge of KV head j's nact chunk partials by one 256-thread workgroup,
+// in batches of 64 chunks. Per batch, the statistics first: one wave per
+// head takes the batch's 64 maxima (a DPP reduction), raises the head's
+// running maximum, and leaves each chunk's weight exp2(M_c - M) in LDS, with
+// the running sum and the factor that rescales the earlier batches. Then the
+// outputs: thread -> 4 consecutive values (quad qd of the G x 64) and slice q
+// of the chunks (c0 + q + NQ b), its weights read as one vector from LDS, one
+// FMA per value and chunk. The loads of the statistics and of the outputs are
+// all issued before the statistics are used (one round trip); chunks past
+// nact load chunk nact - 1 and weigh 0, and the number of output loads per
+// thread is the live count rounded up to 4, 8 or 16. The NQ slices meet in LDS
+// at the end. Every sum runs in a fixed order: the result depends only on the
+// data.
 template <int G>
 __device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid) {
   constexpr int D = kD;
   constexpr int PS = part_stride<G>();
-  constexpr int NQD = G * D / 4;           // quads per chunk
-  constexpr int NQ = kDecThreads / NQD;    // chunk slices
-  constexpr int B = 16;                    // chunks per batch per thread
-  __shared__ float mm_s[kDecThreads], ll_s[kDecThreads];
+  constexpr int CB = 64;                      // chunks per batch
+  constexpr int NQD = G * D / 4;              // output quads per chunk
+  constexpr int NQ = kDecThreads / NQD;       // chunk slices
+  constexpr int PER = CB / NQ;                // chunks per thread per batch
+  constexpr int NE = (CB * G + kDecThreads - 1) / kDecThreads;  // (head, chunk) pairs per thread
+  __shared__ __attribute__((aligned(16))) float w_s[G * CB];    // [head][slice][b]
+  __shared__ float mh_s[G], lh_s[G], sc_s[G];
   __shared__ float4 oo_s[kDecThreads];
+  const int lane = tid & (kWave - 1);
   const int qd = tid % NQD, q = tid / NQD, g = qd / (D / 4);
   const float* base = a.part + static_cast<size_t>(j) * a.head_stride;
-  float M = -INFINITY, Ls = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int k0 = q; k0 < nact; k0 += NQ * B) {
-    float mb[B], lb[B];
-    float4 ob[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {  // clamped chunk index: every load lands in the head's region
-      const float* pk = base + static_cast<size_t>(min(k0 + b * NQ, nact - 1)) * PS;
-      ob[b] = *reinterpret_cast<const float4*>(pk + 4 * qd);
-      mb[b] = pk[G * D + g];
-      lb[b] = pk[G * D + G + g];
-    }
-    float bm = M;
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const bool live = k0 + b * NQ < nact;
-      mb[b] = live ? mb[b] : -INFINITY;
-      lb[b] = live ? lb[b] : 0.f;
-      bm = fmaxf(bm, mb[b]);  // finite: chunk k0 < nact is live
-    }
-    const float keep = exp2f(M - bm);  // 0 on the first batch
-    acc.x *= keep;
-    acc.y *= keep;
-    acc.z *= keep;
-    acc.w *= keep;
-    Ls *= keep;
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const float wgt = exp2f(mb[b] - bm);  // 0 for the chunks past nact
-      const bool live = k0 + b * NQ < nact;
-      acc.x = fmaf(wgt, live ? ob[b].x : 0.f, acc.x);
-      acc.y = fmaf(wgt, live ? ob[b].y : 0.f, acc.y);
-      acc.z = fmaf(wgt, live ? ob[b].z : 0.f, acc.z);
-      acc.w = fmaf(wgt, live ? ob[b].w : 0.f, acc.w);
-      Ls = fmaf(wgt, lb[b], Ls);
-    }
-    M = bm;
+  if (tid < G) {
+    mh_s[tid] = -INFINITY;
+    lh_s[tid] = 0.f;
   }
-  mm_s[tid] = M;
-  ll_s[tid] = Ls;
+  __syncthreads();
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto load_o = [&](int c0, int b) {
+    return *reinterpret_cast<const float4*>(base + static_cast<size_t>(min(c0 + q + NQ * b, nact - 1)) * PS + 4 * qd);
+  };
+  // one batch with N (<= 16) output loads per thread per round
+  auto batch = [&](auto n_tag, int c0) {
+    constexpr int N = decltype(n_tag)::value;
+    float st_m[NE], st_l[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int p = tid + kDecThreads * e, h = min(p / CB, G - 1), c = c0 + p % CB;
+      const float* pk = base + static_cast<size_t>(min(c, nact - 1)) * PS;
+      st_m[e] = pk[G * D + h];
+      st_l[e] = pk[G * D + G + h];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // statistics first: their wait leaves the output loads in flight
+    float4 ob[N];
+#pragma unroll
+    for (int b = 0; b < N; ++b) ob[b] = load_o(c0, b);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int p = tid + kDecThreads * e;
+      if (p < CB * G) {  // whole waves: one head each
+        const int h = p / CB, cb = p % CB;
+        const bool live = c0 + cb < nact;
+        const float m = live ? st_m[e] : -INFINITY;
+        const float mb = wave_max(m);  // finite: chunk c0 is live
+        const float mo = mh_s[h];
+        const float mn = fmaxf(mo, mb);
+        const float wgt = exp2_weight(m - mn);  // 0 past nact
+        w_s[(h * NQ + cb % NQ) * PER + cb / NQ] = wgt;
+        const float ls = wave_sum(live ? wgt * st_l[e] : 0.f);
+        if (lane == 0) {
+          const float sc = exp2_weight(mo - mn);  // 0 on the first batch
+          sc_s[h] = sc;
+          mh_s[h] = mn;
+          lh_s[h] = fmaf(lh_s[h], sc, ls);
+        }
+      }
+    }
+    __syncthreads();
+    const float sc = sc_s[g];
+    acc.x *= sc;
+    acc.y *= sc;
+    acc.z *= sc;
+    acc.w *= sc;
+    const float* wrow = &w_s[(g * NQ + q) * PER];
+#pragma unroll
+    for (int b0 = 0; b0 < PER; b0 += N) {
+      if (b0 > 0) {
+        if (c0 + q + NQ * b0 >= nact) break;  // no live chunk left in this slice
+#pragma unroll
+        for (int b = 0; b < N; ++b) ob[b] = load_o(c0, b0 + b);
+      }
+      float wv[N];
+#pragma unroll
+      for (int b = 0; b < N; b += 4) {
+        const float4 t = *reinterpret_cast<const float4*>(wrow + b0 + b);
+        wv[b] = t.x;
+        wv[b + 1] = t.y;
+        wv[b + 2] = t.z;
+        wv[b + 3] = t.w;
+      }
+#pragma unroll
+      for (int b = 0; b < N; ++b) {
+        acc.x = fmaf(wv[b], ob[b].x, acc.x);
+        acc.y = fmaf(wv[b], ob[b].y, acc.y);
+        acc.z = fmaf(wv[b], ob[b].z, acc.z);
+        acc.w = fmaf(wv[b], ob[b].w, acc.w);
+      }
+      if (N < PER && b0 + N >= PER) break;
+      if (N < 16) break;  // a short batch takes one round
+    }
+    __syncthreads();  // w_s and sc_s are rewritten by the next batch
+  };
+  for (int c0 = 0; c0 < nact; c0 += CB) {
+    const int span = (min(CB, nact - c0) + NQ - 1) / NQ;  // live chunks per slice (uniform)
+    if (span <= 4 && PER >= 4)
+      batch(std::integral_constant<int, (PER < 4 ? PER : 4)>{}, c0);
+    else if (span <= 8 && PER >= 8)
+      batch(std::integral_constant<int, 8>{}, c0);
+    else
+      batch(std::integral_constant<int, (PER < 16 ? PER : 16)>{}, c0);
+  }
   oo_s[tid] = acc;
   __syncthreads();
   if (q == 0) {
-    float Mx = M;  // slice 0 holds chunk 0
+    float4 ot = acc;
 #pragma unroll
-    for (int qq = 1; qq < NQ; ++qq) Mx = fmaxf(Mx, mm_s[qq * NQD + qd]);
-    float lt = 0.f;
-    float4 ot = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int qq = 0; qq < NQ; ++qq) {
-      const float wgt = exp2f(mm_s[qq * NQD + qd] - Mx);  // 0 for an empty slice
+    for (int qq = 1; qq < NQ; ++qq) {
       const float4 o = oo_s[qq * NQD + qd];
-      lt = fmaf(wgt, ll_s[qq * NQD + qd], lt);
-      ot.x = fmaf(wgt, o.x, ot.x);
-      ot.y = fmaf(wgt, o.y, ot.y);
-      ot.z = fmaf(wgt, o.z, ot.z);
-      ot.w = fmaf(wgt, o.w, ot.w);
+      ot.x += o.x;
+      ot.y += o.y;
+      ot.z += o.z;
+      ot.w += o.w;
     }
-    const uint32_t lo = static_cast<uint32_t>(f32_to_bf16(ot.x / lt)) | (static_cast<uint32_t>(f32_to_bf16(ot.y / lt)) << 16);
-    const uint32_t hi = static_cast<uint32_t>(f32_to_bf16(ot.z / lt)) | (static_cast<uint32_t>(f32_to_bf16(ot.w / lt)) << 16);
+    const float rl = __builtin_amdgcn_rcpf(lh_s[g]);
+    const uint32_t lo = cvt_pk_bf16(ot.x * rl, ot.y * rl), hi = cvt_pk_bf16(ot.z * rl, ot.w * rl);
     *reinterpret_cast<uint2*>(a.out + static_cast<size_t>(j) * G * D + 4 * qd) = make_uint2(lo, hi);
   }
 }
