@@ -18,6 +18,7 @@
 //              silu(W.x) * (W2.x)   (the SwiGLU gate/up pair)
 //   residual : added to the (activated) result before the bf16 rounding
 #include "iron_common.hpp"
+#include "i4_dot.hpp"
 #include "../../include/iron_hip.h"
 
 namespace iron {
@@ -63,22 +64,13 @@ __device__ __forceinline__ float dot_chunk(uint4 w, uint4 x, float acc) {
   return acc;
 }
 
-__device__ __forceinline__ float sumsq_chunk(uint4 v, float acc) {
-  float a;
-  a = lo_bf16(v.x); acc = fmaf(a, a, acc); a = hi_bf16(v.x); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.y); acc = fmaf(a, a, acc); a = hi_bf16(v.y); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.z); acc = fmaf(a, a, acc); a = hi_bf16(v.z); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.w); acc = fmaf(a, a, acc); a = hi_bf16(v.w); acc = fmaf(a, a, acc);
-  return acc;
-}
-
 // inv_rms of a K-vector (K % 8 == 0), computed by one wave (all lanes get it).
 __device__ __forceinline__ float wave_inv_rms(const uint16_t* x, int K, float eps, int lane) {
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   float ss = 0.f;
   for (int c = lane; c < (K >> 3); c += kWave) ss = sumsq_chunk(xv[c], ss);
   ss = wave_sum(ss);
-  return rsqrtf(ss / static_cast<float>(K) + eps);
+  return inv_rms(ss, K, eps);
 }
 
 // Final value of one output row (activation or SwiGLU, residual), stored as
@@ -159,7 +151,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
       float ss = 0.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) ss = sumsq_chunk(xc[u], ss);
-      inv = rsqrtf(wave_sum(ss) / static_cast<float>(a.K) + a.eps);
+      inv = inv_rms(wave_sum(ss), a.K, a.eps);
     }
     if (NM == NORM_WEIGHT) {
       const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w) + lane;
@@ -271,14 +263,8 @@ int launch_gemv_bf16(const GemvArgs& a, int norm_mode, int batches, hipStream_t 
 // ---------------------------------------------------------------------------
 // int4, group 32. codes (M, K/2) uint8, two weights per byte along K, low
 // nibble first; scales (M, K/32) bf16. One 16-byte chunk of codes is exactly
-// one group, so lane l owns groups l, l+64, ... of every row it touches.
-//
-// Dequant-free inner product: a nibble n placed in the mantissa of the bf16
-// 0x4300 (=128) gives the exact value 128+n, so one v_bitop3_b32 builds two
-// such weights at once and v_dot2c consumes them. For signed codes the nibble
-// sign bit is flipped in the same op (offset binary, 128+(q+8) = 136+q). The
-// constant part is removed per group with the group's x sum:
-// sum((c+q) x) - c*sum(x). The group scale multiplies the group total once.
+// one group, so lane l owns groups l, l+64, ... of every row it touches. The
+// group inner products are dequant-free (i4_dot.hpp).
 // ---------------------------------------------------------------------------
 struct I4Args {
   const uint8_t* codes;
@@ -297,50 +283,6 @@ struct I4Args {
   float offset;    // 136 signed, 128 unsigned
   int xcd;         // 1: XCD-contiguous row order (xcd_block)
 };
-
-// x chunk of one group (32 bf16) rearranged into the nibble-pair order:
-// word q of the codes holds elements 8q..8q+7; the pair extracted at shift 4j
-// is (element 8q+j, element 8q+j+4).
-struct XGroup {
-  uint32_t p[16];
-  float sum;
-};
-
-__device__ __forceinline__ void build_xgroup(const uint4 (&xc)[4], XGroup& g) {
-  float s = 0.f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t w0 = xc[q].x, w1 = xc[q].y, w2 = xc[q].z, w3 = xc[q].w;  // (x0,x1) (x2,x3) (x4,x5) (x6,x7)
-    g.p[q * 4 + 0] = (w0 & 0xffffu) | (w2 << 16);      // (x0, x4)
-    g.p[q * 4 + 1] = (w0 >> 16) | (w2 & 0xffff0000u);  // (x1, x5)
-    g.p[q * 4 + 2] = (w1 & 0xffffu) | (w3 << 16);      // (x2, x6)
-    g.p[q * 4 + 3] = (w1 >> 16) | (w3 & 0xffff0000u);  // (x3, x7)
-    s += lo_bf16(w0) + hi_bf16(w0) + lo_bf16(w1) + hi_bf16(w1) + lo_bf16(w2) + hi_bf16(w2) + lo_bf16(w3) +
-         hi_bf16(w3);
-  }
-  g.sum = s;
-}
-
-// Truth table of f(a, b, c) = (a & b) ^ c for v_bitop3_b32 (inputs 0xF0, 0xCC, 0xAA).
-constexpr unsigned kAndXor = (0xF0u & 0xCCu) ^ 0xAAu;
-
-// `magic` = 0x43084308 for signed codes (mask, then XOR sets the 0x4300
-// exponent bits and flips the nibble sign bit: 128 + (q + 8)), 0x43004300 for
-// unsigned codes (128 + n). One v_bitop3_b32 + one v_dot2c per weight pair.
-__device__ __forceinline__ float i4_group_dot(uint4 c, const XGroup& g, uint32_t magic) {
-  const uint32_t words[4] = {c.x, c.y, c.z, c.w};
-  float acc = 0.f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t u = words[q];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t wpair = __builtin_amdgcn_bitop3_b32(u >> (4 * j), 0x000f000fu, magic, kAndXor);
-      acc = dot2_bf16(wpair, g.p[q * 4 + j], acc);
-    }
-  }
-  return acc;
-}
 
 // Fast path: K == 2048*GPL*KS. The 4 waves of a workgroup form 4/KS row
 // groups of R rows; the KS waves of a row group split K, each lane owning GPL
@@ -413,7 +355,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[j][q], ss);
       ss = wave_sum(ss);
-      if (KS == 1) inv = rsqrtf(ss / static_cast<float>(a.K) + a.eps);
+      if (KS == 1) inv = inv_rms(ss, a.K, a.eps);
     }
     if (NM == NORM_WEIGHT) {
       if (KS > 1) {  // the full sum of squares is needed before the products
@@ -423,7 +365,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < KS; ++k) t += ss_s[rg * KS + k];
-        inv = rsqrtf(t / static_cast<float>(a.K) + a.eps);
+        inv = inv_rms(t, a.K, a.eps);
       }
 #pragma unroll
       for (int j = 0; j < GPL; ++j)
@@ -439,10 +381,10 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       float acc = 0.f, acc2 = 0.f;
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
-        const float d = i4_group_dot(cw[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+        const float d = i4_group_total(cw[r][j], xg[j], a.magic, a.offset);
         acc = fmaf(bf16_to_f32(sc[r][j]), d, acc);
         if (PAIR) {
-          const float d2 = i4_group_dot(cw2[r][j], xg[j], a.magic) - a.offset * xg[j].sum;
+          const float d2 = i4_group_total(cw2[r][j], xg[j], a.magic, a.offset);
           acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
         }
       }
@@ -474,7 +416,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       float t = ss;
 #pragma unroll
       for (int k = 1; k < KS; ++k) t += q_s[wave + k];
-      inv = rsqrtf(t / static_cast<float>(a.K) + a.eps);
+      inv = inv_rms(t, a.K, a.eps);
     }
   }
   unsigned long long key = 0;
@@ -529,8 +471,8 @@ __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) 
       }
       XGroup t;
       build_xgroup(xc, t);
-      acc = fmaf(s, i4_group_dot(c, t, a.magic) - a.offset * t.sum, acc);
-      if (PAIR) acc2 = fmaf(s2, i4_group_dot(c2, t, a.magic) - a.offset * t.sum, acc2);
+      acc = fmaf(s, i4_group_total(c, t, a.magic, a.offset), acc);
+      if (PAIR) acc2 = fmaf(s2, i4_group_total(c2, t, a.magic, a.offset), acc2);
     }
     float t = wave_sum(acc);
     float t2 = PAIR ? wave_sum(acc2) : 0.f;

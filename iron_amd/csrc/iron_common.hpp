@@ -119,6 +119,14 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 1 / sqrt(ss / n + eps) by one v_rsq_f32 (relative error ~1 ulp), the RMS
+// scale of the GEMVs' fused norms: one instruction instead of a square root
+// and a full division, and the same bits in every kernel variant whatever
+// its compile flags.
+__device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
+  return __builtin_amdgcn_rsqf(ss / static_cast<float>(n) + eps);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
