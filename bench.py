@@ -450,6 +450,22 @@ def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0):
                         "TFLOP/s", "config-5 prefill GEMM 512x2048x8192 via oracle.ops.gemm_reference (torch CPU, fp32)")
     res = _gpu_line("prefill_gemm" + ("_int4" if int4 else ""), t, flops=2.0 * M * N * K, cpu=cpu)
     res.update({"shape": [M, K, N], "weights": "int4-g32" if int4 else "bf16", "weight_copies": copies})
+    if not int4:
+        # the vendor library on the same shape and protocol: torch.matmul -> hipBLASLt (a 2-D product of a
+        # transposed weight view; no batched kernel involved)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+        def launch_lib(i, s):
+            torch.matmul(A, Ws[i % copies].t(), out=out)
+
+        for i in range(10):
+            launch_lib(i, stream)
+        torch.cuda.synchronize()
+        t_lib = tm.rotating_us(launch_lib, copies, n)
+        tf = 2.0 * M * N * K / t_lib / 1e6
+        res["library_reference"] = {"what": "torch.matmul (hipBLASLt), same shape, same weight rotation",
+                                    "kernel_us": round(t_lib, 3), "TFLOP/s": round(tf, 1),
+                                    "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
     return res
 
 
