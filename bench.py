@@ -738,7 +738,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
-    ap.add_argument("--mode", choices=["full", "gemv", "model", "prefill", "attention", "floor", "mfma"],
+    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "attention", "floor", "mfma"],
                     default="full")
     args = ap.parse_args()
 
@@ -778,6 +778,8 @@ def main() -> int:
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
             "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608),
         })
+    if args.mode == "gemv_bf16":
+        return emit("gemv_bf16", {"gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300)})
     if args.mode == "floor":
         return emit("floor", {"floor": bench_floor(torch, lib, tm, dev)})
     if args.mode == "mfma":
