@@ -2,12 +2,13 @@
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--mode full|gemv|model|prefill|attention|floor]
+                    [--mode full|gemv|gemv_bf16|model|prefill|gemm_large|attention|floor|mfma]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
 runs only the Llama configuration; --mode prefill only the config 5 prefill
-GEMM and the 3968-token causal attention; --mode attention the GQA decode
+GEMM and the 3968-token causal attention; --mode gemm_large the 3968-token
+prefill projections and 4096^3 beside hipBLASLt; --mode attention the GQA decode
 attention at config 3 and at KV 4096; --mode floor the per-launch floors (an
 empty kernel as a graph node, a pure streaming read of the decode kernels'
 sizes). The modes exist for kernel traces and counters.
@@ -408,14 +409,15 @@ def bench_swiglu(torch, lib, tm, dev, n, cpu_s=0.0):
     return res
 
 
-def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0):
+def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0, shape=(512, 2048, 8192)):
     """Config 5 prefill GEMM M=512 K=2048 N=8192 (bf16 weights, or int4-g32
     weights dequantised in the kernel's prologue), weights rotated through the
-    pool (cold, as in the model, where each layer's weights are read once)."""
+    pool (cold, as in the model, where each layer's weights are read once).
+    `shape` = (M, K, N) times another bf16 projection the same way."""
     from iron_amd import _lib
     from oracle import ops
 
-    M, K, N = 512, 2048, 8192
+    M, K, N = shape
     g = torch.Generator(device=dev).manual_seed(0)
     A = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
     W = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
@@ -738,7 +740,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
-    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "attention", "floor", "mfma"],
+    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "gemm_large", "attention", "floor",
+                                       "mfma"],
                     default="full")
     args = ap.parse_args()
 
@@ -773,6 +776,12 @@ def main() -> int:
             "prefill_gemm_int4_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, int4=True),
             "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
         })
+    if args.mode == "gemm_large":
+        # the 3968-token prefill projections (o_proj, qkv, down, fused gate/up pair) and 4096^3, each beside
+        # hipBLASLt on the same shape and weight rotation
+        shapes = {"o_proj_3968": (3968, 2048, 2048), "qkv_3968": (3968, 2048, 3072), "down_3968": (3968, 8192, 2048),
+                  "gate_up_3968": (3968, 2048, 16384), "square_4096": (4096, 4096, 4096)}
+        return emit("gemm_large", {k: bench_prefill_gemm(torch, lib, tm, dev, 10, shape=v) for k, v in shapes.items()})
     if args.mode == "attention":
         return emit("attention", {
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
