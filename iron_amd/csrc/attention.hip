@@ -772,12 +772,12 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   // loads 1 KiB blocks 4w..4w+3 (0-7 K, 8-15 V). Lane l lands on row
   // 8 (b % 8) + l / 8, slot l % 8 and fetches the chunk that belongs there.
   // Keys past Skv load key Skv-1: finite values whose weights are zero.
-  // Blocks are issued in order 0, 1, 2, ...: each lane keeps the source of
-  // its next row and bumps it by 64 rows per issue; only a block that runs
-  // past Skv recomputes clamped addresses.
-  const uint16_t* src[4];
-  const uint16_t* next_src[4];
-  long long rstride[4];
+  // Blocks are issued in order 0, 1, 2, ...: each lane keeps the byte offset of
+  // its next row (from the head's K or V base, through a buffer resource: see
+  // load_lds16) and bumps it by 64 rows per issue; only a block that runs past
+  // Skv recomputes clamped offsets.
+  const i32x4v rsrc_k = buffer_rsrc(a.k + hk * a.k_hs), rsrc_v = buffer_rsrc(a.v + hk * a.v_hs);
+  unsigned coff[4], rsb[4], next_off[4];
   int lrow[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -785,20 +785,19 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     const bool is_k = b < 8;
     const int r = (b & 7) * 8 + (lane >> 3), slot = lane & 7;
     const int chunk = is_k ? fa_k_slot(r, slot) : fa_v_slot(r, slot);  // both are involutions
-    src[j] = (is_k ? a.k + hk * a.k_hs : a.v + hk * a.v_hs) + chunk * 8;
-    rstride[j] = is_k ? a.k_rs : a.v_rs;
+    coff[j] = chunk * 16;
+    rsb[j] = static_cast<unsigned>((is_k ? a.k_rs : a.v_rs) * 2);
     lrow[j] = r;
-    next_src[j] = src[j] + r * rstride[j];
+    next_off[j] = coff[j] + r * rsb[j];
   }
   auto issue = [&](int bi) {
     unsigned char* st = lds + (bi % kFaStages) * 2 * kFaBlock;
     const bool inside = bi * kFaK + kFaK <= a.Skv;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint16_t* p = inside ? next_src[j] : src[j] + min(bi * kFaK + lrow[j], a.Skv - 1) * rstride[j];
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(p),
-                                       reinterpret_cast<unsigned*>(st + (wave * 4 + j) * 1024), 16, 0, 0);
-      next_src[j] += kFaK * rstride[j];
+      const unsigned off = inside ? next_off[j] : coff[j] + min(bi * kFaK + lrow[j], a.Skv - 1) * rsb[j];
+      load_lds16(wave * 4 + j < 8 ? rsrc_k : rsrc_v, off, st + (wave * 4 + j) * 1024);
+      next_off[j] += kFaK * rsb[j];
     }
   };
   // this lane's transposed-read address inside a V block: 16-lane group g
@@ -1175,6 +1174,9 @@ extern "C" int iron_attention_prefill(const void* q, const void* k, const void* 
   IRON_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && q_row_stride % 8 == 0 && q_head_stride % 8 == 0 &&
                    kv_row_stride % 8 == 0 && kv_head_stride % 8 == 0,
                "iron_attention_prefill: rows must be 16-byte aligned");
+  // K/V rows are addressed by 32-bit byte offsets from each head's base
+  IRON_REQUIRE(kv_row_stride >= 0 && static_cast<long long>(seq_kv) * kv_row_stride * 2 < (1LL << 31) - 256,
+               "iron_attention_prefill: seq_kv=%d x kv_row_stride=%lld spans more than 2 GiB", seq_kv, kv_row_stride);
   PrefillArgs a{static_cast<const uint16_t*>(q),
                 static_cast<const uint16_t*>(k),
                 static_cast<const uint16_t*>(v),

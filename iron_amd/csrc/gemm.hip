@@ -51,6 +51,10 @@ typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2v __attribute__((ext_vector_type(2)));
 
 constexpr int BK = 64;
+// Buffer offsets are 32-bit: a tile's rows (at most 256) times K times 2 bytes must stay below 2^31.
+constexpr int kMaxK = 1 << 21;
+
+
 constexpr int kChunks = BK / 8;  // 16-byte chunks per LDS row
 constexpr int kSplitTile = 128;  // tile edge the split-K policy counts in
 // Epilogue of the fused SwiGLU GEMM (iron_gemm_bf16_nt_swiglu); not part of the
@@ -263,24 +267,26 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
   const int nk = a.K / BK / a.splits;  // steps in this workgroup's K range
 
   // The PW blocks this wave loads each step: block b < BM/8 is rows 8b..8b+7
-  // of A, the rest are rows of B. Source pointers at the first step of the range.
-  const uint16_t* src[PW];
+  // of A, the rest are rows of B, through buffer resources based at the tile's
+  // first A row and first B row (load_lds16). off[j]: byte offset of this lane's
+  // chunk at the range's first step.
+  const i32x4v rsrc_a = buffer_rsrc(a.A + static_cast<size_t>(m0) * a.K);
+  const i32x4v rsrc_b = buffer_rsrc(a.B + static_cast<size_t>(n0) * a.K);
+  unsigned off[PW];
 #pragma unroll
   for (int j = 0; j < PW; ++j) {
     const int b = wave * PW + j;
     const bool is_a = b < BM / 8;
     const int row = (is_a ? b : b - BM / 8) * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-    const size_t k0 = static_cast<size_t>(kb) * nk * BK + chunk * 8;
-    src[j] = is_a ? a.A + static_cast<size_t>(min(m0 + row, a.M - 1)) * a.K + k0
-                  : a.B + static_cast<size_t>(min(n0 + row, a.N - 1)) * a.K + k0;
+    const int r = is_a ? min(m0 + row, a.M - 1) - m0 : min(n0 + row, a.N - 1) - n0;
+    off[j] = static_cast<unsigned>((r * a.K + kb * nk * BK + chunk * 8) * 2);
   }
   auto issue = [&](int step) {
-    u32x4v* st = smem + (step % NS) * T::kStage;
 #pragma unroll
     for (int j = 0; j < PW; ++j)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const unsigned*>(src[j] + step * BK),
-                                       reinterpret_cast<unsigned*>(st + (wave * PW + j) * 64), 16, 0, 0);
+      load_lds16(wave * PW + j < BM / 8 ? rsrc_a : rsrc_b, off[j] + step * BK * 2,
+                 smem + (step % NS) * T::kStage + (wave * PW + j) * 64);
   };
 
   f32x16_t acc[TI][TJ];
@@ -638,6 +644,7 @@ static int gemm_check(const char* fn, const void* A, const void* B, const void* 
   IRON_REQUIRE(A && B && C, "%s: null pointer", fn);
   IRON_REQUIRE(M > 0 && N > 0 && K > 0, "%s: M=%d N=%d K=%d must be positive", fn, M, N, K);
   IRON_REQUIRE(K % BK == 0, "%s: K=%d must be a multiple of %d", fn, K, BK);
+  IRON_REQUIRE(K <= kMaxK, "%s: K=%d exceeds %d", fn, K, kMaxK);
   IRON_REQUIRE(aligned16(A) && aligned16(B), "%s: A and B must be 16-byte aligned", fn);
   IRON_REQUIRE(ldc >= N, "%s: ldc=%lld < N=%d", fn, ldc, N);
   const int act = epilogue & ~IRON_EPI_ROUND_TOWARD_ZERO;

@@ -47,6 +47,36 @@ __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w 
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) { return cvt_pk_bf16(lo, hi); }
 
+// Word 3 of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
+constexpr int kBufferFlags = 0x00020000;
+
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (V#) over the bytes from `base`: 32-bit offsets, no stride,
+// no range check beyond 2^31 - 1 bytes.
+__device__ __forceinline__ i32x4v buffer_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4v r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
+  r[2] = 0x7fffffff;
+  r[3] = kBufferFlags;
+  return r;
+}
+
+// buffer_load_dwordx4 ... lds: 16 bytes per lane from rsrc + voffset into LDS at
+// lds (the wave's base; lane l lands at lds + 16 l). Written as assembly: while a
+// global_load_lds it issued is in flight, the compiler can only wait for every
+// outstanding LDS read at once (lgkmcnt(0)) before using any of them; with loads
+// it does not see, it keeps exact counts (lgkmcnt(N)), so LDS reads issued ahead
+// overlap the work before their use. The caller orders completion with its own
+// s_waitcnt vmcnt and barriers.
+__device__ __forceinline__ void load_lds16(const i32x4v& rsrc, unsigned voffset, const void* lds) {
+  const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(rsrc)
+               : "memory", "m0");
+}
+
 // Argmax key: unsigned order of (value, -index), so the largest key is the
 // largest value and, among equal values, the smallest index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
