@@ -85,7 +85,11 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), sources))
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    # --no-undefined: a kernel whose host-side launch stub was silently not emitted
+    # (the host pass drops a template kernel whose body it cannot instantiate) fails here
+    # instead of at dlopen on the GPU box
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", str(tmp),
+           *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
