@@ -70,7 +70,10 @@ __device__ __forceinline__ i32x4v buffer_rsrc(const void* base) {
 // outstanding LDS read at once (lgkmcnt(0)) before using any of them; with loads
 // it does not see, it keeps exact counts (lgkmcnt(N)), so LDS reads issued ahead
 // overlap the work before their use. The caller orders completion with its own
-// s_waitcnt vmcnt and barriers.
+// s_waitcnt vmcnt and barriers. M0 is written behind the compiler's back (it
+// does not preserve a reserved register named as clobbered), so the calling
+// kernel must be one in which the compiler itself never uses M0: no LDS-direct
+// builtins and no M0-indexed instructions (checked in the kernels' assembly).
 __device__ __forceinline__ void load_lds16(const i32x4v& rsrc, unsigned voffset, const void* lds) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(rsrc)
