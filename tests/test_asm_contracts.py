@@ -1,0 +1,71 @@
+"""Contracts of hand-written assembly that the compiler cannot check, verified
+on the gfx950 assembly of this repository's own sources (no GPU needed).
+
+load_lds16 (iron_common.hpp) writes M0 behind the compiler's back: in every
+kernel that uses it, each M0 write must be its own (the instruction right after
+it is its buffer_load ... lds), so the compiler never keeps a value of its own
+in M0 there.
+"""
+
+import re
+import subprocess
+
+import pytest
+
+from iron_amd import _build
+
+KERNELS = {
+    "gemm.hip": ["gemm_nt_kernel"],
+    "attention.hip": ["attention_prefill_kernel"],
+}
+
+
+def device_asm(src_name):
+    try:
+        hipcc = _build._hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    src = _build.CSRC / src_name
+    cmd = [hipcc, *_build.HIP_FLAGS, *_build.FILE_FLAGS.get(src_name, []), "--cuda-device-only", "-S", str(src),
+           "-o", "-"]
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, out.stderr[-2000:]
+    return out.stdout
+
+
+def functions(asm):
+    """name -> list of instruction lines of each function in the assembly."""
+    funcs, name, body = {}, None, []
+    for line in asm.splitlines():
+        m = re.match(r"^(_Z\S+):", line)
+        if m:
+            name, body = m.group(1), []
+            funcs[name] = body
+            continue
+        if name is not None:
+            s = line.split(";")[0].strip()
+            if s and not s.startswith("."):
+                body.append(s)
+            if s.startswith("s_endpgm"):
+                name = None
+    return funcs
+
+
+@pytest.mark.parametrize("src_name", sorted(KERNELS))
+def test_m0_written_only_by_load_lds16(src_name):
+    funcs = functions(device_asm(src_name))
+    checked = 0
+    for fname, body in funcs.items():
+        if not any(k in fname for k in KERNELS[src_name]):
+            continue
+        checked += 1
+        loads = 0
+        for i, ins in enumerate(body):
+            if re.search(r"\bm0\b", ins):
+                assert ins.startswith("s_mov_b32 m0,"), (fname, i, ins)
+                nxt = body[i + 1] if i + 1 < len(body) else ""
+                assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith("lds"), (fname, i, ins, nxt)
+                loads += 1
+        assert loads > 0, fname
+        assert not any(ins.startswith("global_load_lds") for ins in body), fname
+    assert checked > 0, f"no kernel of {KERNELS[src_name]} found in {src_name}"
