@@ -232,7 +232,9 @@ int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new,
  * (element strides per head and per row; rows 16-byte aligned). Query row i
  * sits at position q_offset+i; with causal it sees keys <= that position.
  * fp32 online softmax. Rows [Sq, out_rows) of out are written as zeros (the
- * MHA operator's padded layout); pass out_rows <= Sq for none. Replaces MHA.get_callable() -> (Q, K, V, O):
+ * MHA operator's padded layout); pass out_rows <= Sq for none. K/V rows are
+ * addressed by 32-bit byte offsets from each head's base: seq_kv *
+ * kv_row_stride * 2 must stay below 2 GiB. Replaces MHA.get_callable() -> (Q, K, V, O):
  * iron/operators/mha/op.py:21-135, golden mha/reference.py:27-94, and the
  * CPU prefill attention of llama_npu.py:948-990. */
 int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads, int n_kv_heads,
@@ -244,8 +246,8 @@ int iron_attention_prefill(const void* q, const void* k, const void* v, void* ou
 /* ---------------------------------------------------------------- GEMM ---- */
 
 /* C = clamp(act(bf16(A . B^T))) on bf16 MFMA, fp32 accumulation:
- * A (M,K), B (N,K) both K-contiguous (K % 64 == 0, 16-byte aligned), C (M,N)
- * with row stride ldc. epilogue: enum iron_epilogue (applied after the bf16
+ * A (M,K), B (N,K) both K-contiguous (K % 64 == 0, K <= 2^21, 16-byte
+ * aligned), C (M,N) with row stride ldc. epilogue: enum iron_epilogue (applied after the bf16
  * rounding of the accumulator); has_clamp clamps to [clamp_lo, clamp_hi].
  * Replaces GEMM.get_callable() -> (A, B, C) of iron/operators/gemm/op.py:21-231
  * (b_col_maj=True; other layouts via iron_transpose_bf16 / operand swap) and
