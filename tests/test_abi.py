@@ -110,3 +110,16 @@ def test_gqa_decode_noalloc_rejects_oversized_shape_on_host():
                   None)
     with pytest.raises(_lib.IronHipError, match="invalid shape"):
         _lib.call("iron_gqa_decode_noalloc", 16, 16, 16, 16, 16, 16, 128, 16, 32, 8, 32, 128, 0, None, 0.125, None)
+
+
+def test_offset_limits_rejected_on_host():
+    """Arguments past the kernels' 32-bit buffer offsets are rejected before any launch:
+    GEMM K above 2^21, prefill-attention K/V spans of 2 GiB or more."""
+    from iron_amd import _lib
+
+    p = 1 << 20  # a 16-byte-aligned stand-in address: nothing is launched
+    with pytest.raises(_lib.IronHipError, match="exceeds"):
+        _lib.call("iron_gemm_bf16_nt", p, p, p, 64, 64, (1 << 21) + 64, 64, 0, 0, 0.0, 0.0, None)
+    with pytest.raises(_lib.IronHipError, match="2 GiB"):
+        _lib.call("iron_attention_prefill", p, p, p, p, 8, 8, 16, 1 << 20, 64, 64, 512, 64, 1 << 10, 64, 512, 16, 1, 0,
+                  0.125, None)
