@@ -136,6 +136,19 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
   constexpr int BM = T::BM, BN = T::BN, TI = T::TI, TJ = T::TJ;
   if (a.partial) {  // split-K: raw fp32 sums straight from the accumulators
     float* P = a.partial + static_cast<size_t>(kb) * a.M * a.N;
+    if (m0 + BM <= a.M && n0 + BN <= a.N) {  // the whole tile is inside (uniform): no per-element tests
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int gm = m0 + wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            const int gn = n0 + wn * TJ * 32 + j * 32 + (lane & 31);
+            P[static_cast<size_t>(gm) * a.N + gn] = acc[i][j][v];
+          }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
@@ -153,22 +166,38 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
   __syncthreads();  // every wave is done reading the last stage
   uint16_t* Cs = reinterpret_cast<uint16_t*>(smem);
   const bool swiglu = a.epi == kEpiSwigluPair;
+  // The epilogue's options are uniform: branch once on them, not per element
+  // (per-element tests of the activation, clamp and rounding mode cost more
+  // than the conversions, and this loop runs with the CU otherwise idle).
+  if ((swiglu || (a.epi == EPI_NONE && !a.clamp)) && !a.toward_zero) {
 #pragma unroll
-  for (int i = 0; i < TI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j)
+      for (int j = 0; j < TJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const int col = wn * TJ * 32 + j * 32 + (lane & 31);
-        float x = acc[i][j][v];
-        if (!swiglu && (a.epi != EPI_NONE || a.clamp)) {
-          x = bf16_to_f32(out_bf16(x, a.toward_zero));
-          x = apply_epilogue(x, a.epi);
-          if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
+        for (int v = 0; v < 16; ++v) {
+          const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const int col = wn * TJ * 32 + j * 32 + (lane & 31);
+          Cs[row * BN + col] = f32_to_bf16(acc[i][j][v]);
         }
-        Cs[row * BN + col] = out_bf16(x, a.toward_zero);
-      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = wm * TI * 32 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const int col = wn * TJ * 32 + j * 32 + (lane & 31);
+          float x = acc[i][j][v];
+          if (!swiglu && (a.epi != EPI_NONE || a.clamp)) {
+            x = bf16_to_f32(out_bf16(x, a.toward_zero));
+            x = apply_epilogue(x, a.epi);
+            if (a.clamp) x = fminf(fmaxf(x, a.lo), a.hi);
+          }
+          Cs[row * BN + col] = out_bf16(x, a.toward_zero);
+        }
+  }
   __syncthreads();
   if (swiglu) {
     // Column blocks 2p and 2p+1 of 64 hold gate and up of features
@@ -177,6 +206,25 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
     constexpr int CH = BN / 16;  // 8-feature chunks per output row
     const int F = a.N / 2;
     const bool full_f = (n0 / 2 + BN / 2 <= F) && (a.ldc % 8 == 0);
+    auto h_chunk = [&](int row, int c) {  // 8 features of one row: silu(g) * u, packed bf16
+      const int gcol = (c / 8) * 128 + (c % 8) * 8;
+      const uint4 gv = reinterpret_cast<const uint4*>(Cs)[(row * BN + gcol) / 8];
+      const uint4 uv = reinterpret_cast<const uint4*>(Cs)[(row * BN + gcol + 64) / 8];
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        h[e] = cvt_pk_bf16(silu_f32(lo_bf16(gw[e])) * lo_bf16(uw[e]), silu_f32(hi_bf16(gw[e])) * hi_bf16(uw[e]));
+      return make_uint4(h[0], h[1], h[2], h[3]);
+    };
+    if (full_f && m0 + BM <= a.M) {  // the whole tile is inside H (uniform)
+#pragma unroll
+      for (int i = 0; i < (BM * CH) / T::kThreads; ++i) {
+        const int id = tid + i * T::kThreads, row = id / CH, c = id % CH;
+        *reinterpret_cast<uint4*>(a.C + static_cast<size_t>(m0 + row) * a.ldc + n0 / 2 + c * 8) = h_chunk(row, c);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < (BM * CH) / T::kThreads; ++i) {
       const int id = tid + i * T::kThreads, row = id / CH, c = id % CH;
@@ -201,6 +249,15 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const f32x16_t (&a
     return;
   }
   const bool full_n = (n0 + BN <= a.N) && (a.ldc % 8 == 0);
+  if (full_n && m0 + BM <= a.M) {  // the whole tile is inside C (uniform)
+#pragma unroll
+    for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
+      const int id = tid + i * T::kThreads, row = id / (BN / 8), c = id % (BN / 8);
+      *reinterpret_cast<uint4*>(a.C + static_cast<size_t>(m0 + row) * a.ldc + n0 + c * 8) =
+          reinterpret_cast<const uint4*>(Cs)[row * (BN / 8) + c];
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < (BM * BN / 8) / T::kThreads; ++i) {
     const int id = tid + i * T::kThreads, row = id / (BN / 8), c = id % (BN / 8);
