@@ -74,9 +74,13 @@ __device__ __forceinline__ i32x4v buffer_rsrc(const void* base) {
 // does not preserve a reserved register named as clobbered), so the calling
 // kernel must be one in which the compiler itself never uses M0: no LDS-direct
 // builtins and no M0-indexed instructions (checked in the kernels' assembly).
+// An LDS-DMA instruction must not directly follow the scalar write of M0 it
+// reads (one wait state on GFX9, which the compiler inserts for its own code
+// but not inside assembly): the s_nop 0 provides it.
 __device__ __forceinline__ void load_lds16(const i32x4v& rsrc, unsigned voffset, const void* lds) {
   const unsigned m0 = __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(lds)));
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset), "s"(rsrc)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voffset),
+               "s"(rsrc)
                : "memory", "m0");
 }
 

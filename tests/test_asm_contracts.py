@@ -2,9 +2,10 @@
 on the gfx950 assembly of this repository's own sources (no GPU needed).
 
 load_lds16 (iron_common.hpp) writes M0 behind the compiler's back: in every
-kernel that uses it, each M0 write must be its own (the instruction right after
-it is its buffer_load ... lds), so the compiler never keeps a value of its own
-in M0 there.
+kernel that uses it, each M0 write must be its own (followed by one wait state,
+s_nop 0, then its buffer_load ... lds), so the compiler never keeps a value of
+its own in M0 there, and no LDS-DMA load directly follows the M0 write it reads
+(GFX9 needs one wait state between the two).
 """
 
 import re
@@ -63,7 +64,9 @@ def test_m0_written_only_by_load_lds16(src_name):
         for i, ins in enumerate(body):
             if re.search(r"\bm0\b", ins):
                 assert ins.startswith("s_mov_b32 m0,"), (fname, i, ins)
-                nxt = body[i + 1] if i + 1 < len(body) else ""
+                nop = body[i + 1] if i + 1 < len(body) else ""
+                nxt = body[i + 2] if i + 2 < len(body) else ""
+                assert nop == "s_nop 0", (fname, i, ins, nop)
                 assert nxt.startswith("buffer_load_dwordx4") and nxt.endswith("lds"), (fname, i, ins, nxt)
                 loads += 1
         assert loads > 0, fname
