@@ -757,6 +757,12 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     for (int kk = 0; kk < 4; ++kk)
       qf[kk] = __builtin_bit_cast(fa_bf16x8, *reinterpret_cast<const fa_u32x4*>(qp + 16 * kk + 8 * hh));
   }
+  // Use the Q fragments here, before any K/V load is issued: the compiler then
+  // waits for these four loads now. Otherwise it counts them as outstanding at
+  // their first use inside the key loop and waits there with vmcnt, which also
+  // drains the K/V blocks the loop keeps in flight (the compiler does not count
+  // those assembly loads).
+  asm volatile("" ::"v"(qf[0]), "v"(qf[1]), "v"(qf[2]), "v"(qf[3]));
   fa_f32x16 o[2];
 #pragma unroll
   for (int j = 0; j < 16; ++j) o[0][j] = o[1][j] = 0.f;
@@ -804,28 +810,45 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   // covers dims 16 (g % 2) .. + 15 (+ 32 db) and keys 4 hh .. + 3 (+ 16 st, + 8)
   const int tr_row = 4 * hh + ((lane & 15) >> 2), tr_dim = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  // S^T = K Q^T for block bi: sc[b][j] is key 64 bi + 32 b + 8 (j / 4) + 4 hh + j % 4, query qw + c
-  auto scores = [&](int bi, fa_f32x16 (&sc)[2]) {
+  // S^T = K Q^T for block bi: sc[b][j] is key 64 bi + 32 b + 8 (j / 4) + 4 hh + j % 4, query qw + c.
+  // k_frags reads the block's K fragments (A operand: key 32 b + c, dims 16 kk + 8 hh .. + 8);
+  // s_mfma runs the two independent accumulation chains (b = 0, 1) interleaved.
+  auto k_frags = [&](int bi, fa_bf16x8 (&kf)[2][4]) {
     const unsigned char* ks = lds + (bi % kFaStages) * 2 * kFaBlock;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      const int kr = 32 * b + c;
-      fa_f32x16 acc = {};  // the first MFMA takes an inline zero accumulator
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const fa_bf16x8 kf = __builtin_bit_cast(
+        const int kr = 32 * b + c;
+        kf[b][kk] = __builtin_bit_cast(
             fa_bf16x8, *reinterpret_cast<const fa_u32x4*>(ks + kr * 128 + fa_k_slot(kr, 2 * kk + hh) * 16));
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], acc, 0, 0, 0);
       }
-      sc[b] = acc;
+  };
+  auto s_mfma = [&](const fa_bf16x8 (&kf)[2][4], fa_f32x16 (&sc)[2]) {
+    fa_f32x16 acc0 = {}, acc1 = {};  // the first MFMAs take an inline zero accumulator
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0][kk], qf[kk], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1][kk], qf[kk], acc1, 0, 0, 0);
     }
+    sc[0] = acc0;
+    sc[1] = acc1;
+  };
+  auto scores = [&](int bi, fa_f32x16 (&sc)[2]) {
+    fa_bf16x8 kf[2][4];
+    k_frags(bi, kf);
+    s_mfma(kf, sc);
   };
   auto visible = [&](int bi) { return !a.causal || bi * kFaK <= wave_last; };
 
-  // Software pipeline over key blocks: iteration bi waits for block bi+1,
-  // issues its S^T MFMAs, then runs block bi's softmax and P V while they
-  // execute. Stages: bi (V being read), bi+1 (K being read), bi+2 in flight,
-  // bi+3 being issued into the stage block bi-1 used.
+  // Software pipeline over key blocks: iteration bi waits for block bi+1 and
+  // reads its K fragments and block bi's V^T fragments, takes block bi's row
+  // maximum, then runs block bi+1's S^T MFMAs, block bi's exponentials and its
+  // P V MFMAs in one branch-free stretch, so that the matrix cores work while
+  // the softmax occupies the VALU. Stages: bi (V being read), bi+1 (K being
+  // read), bi+2 in flight, bi+3 being issued into the stage block bi-1 used.
+  // On the last iteration the K fragments come from a stage no load writes any
+  // more and the scores they give are not used.
 #pragma unroll
   for (int p = 0; p < kFaStages - 1; ++p)
     if (p < nb) issue(p);
@@ -837,7 +860,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
   else
     fa_wait_loads_barrier<0>();
   fa_f32x16 sa[2], sb[2];
-  if (visible(0)) scores(0, sa);
+  scores(0, sa);  // block 0 is visible to every wave
 
   auto step = [&](int bi, fa_f32x16 (&cur)[2], fa_f32x16 (&nxt)[2]) {
     if (bi + 1 < nb) {
@@ -847,9 +870,10 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
         fa_wait_loads_barrier<0>();
       // block bi-1's stage is free: every wave passed this barrier after its last read of it
       if (bi + kFaStages - 1 < nb) issue(bi + kFaStages - 1);
-      if (visible(bi + 1)) scores(bi + 1, nxt);
     }
-    if (!visible(bi)) return;  // every key of the block is after this wave's queries
+    if (!visible(bi)) return;  // every key of the block (and of the next) is after this wave's queries
+    fa_bf16x8 kf[2][4];
+    k_frags(bi + 1, kf);  // waited for with the V^T reads below
     const int k0 = bi * kFaK;
     const unsigned char* vs = lds + (bi % kFaStages) * 2 * kFaBlock + kFaBlock;
       // V^T fragments for O^T += V^T P^T, read while the next block's S^T MFMAs run: k-step st,
@@ -903,10 +927,13 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
             mx = fmaxf(mx, cur[b][j]);
           }
       } else {
+        mx = fmaxf(fmaxf(cur[0][0], cur[0][1]), cur[0][2]);  // a chain of v_max3_f32
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int j = 3; j < 15; j += 2) mx = fmaxf(fmaxf(mx, cur[0][j]), cur[0][j + 1]);
+        mx = fmaxf(fmaxf(mx, cur[0][15]), cur[1][0]);
 #pragma unroll
-          for (int j = 0; j < 16; j += 2) mx = fmaxf(mx, fmaxf(cur[b][j], cur[b][j + 1]));  // v_max3_f32
+        for (int j = 1; j < 15; j += 2) mx = fmaxf(fmaxf(mx, cur[1][j]), cur[1][j + 1]);
+        mx = fmaxf(mx, cur[1][15]);
       }
       mx = fa_pair_max(mx);
       // Lazy rescaling: the running maximum m moves only when this block's
@@ -926,6 +953,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
         }
       }
       const float moff = (m == -INFINITY) ? 0.f : m;  // keeps 2^(-inf - moff) = 0, never NaN
+      s_mfma(kf, nxt);  // block bi+1's scores, independent of everything below
       // P^T fragments: pf[2 b + sp] element i = register 8 sp + i of s[b]
       fa_bf16x8 pf[4];
       float psum = 0.f;
