@@ -876,38 +876,26 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     k_frags(bi + 1, kf);  // waited for with the V^T reads below
     const int k0 = bi * kFaK;
     const unsigned char* vs = lds + (bi % kFaStages) * 2 * kFaBlock + kFaBlock;
-      // V^T fragments for O^T += V^T P^T, read while the next block's S^T MFMAs run: k-step st,
-      // element i of lane (d, hh) is key 16 st + 8 (i / 4) + 4 hh + i % 4 (two
-      // transposed reads of 4 keys each). The reads are inline assembly ending in
-      // their own lgkmcnt wait: as a builtin, the compiler makes the first one wait
-      // for every LDS-direct load in flight (it cannot tell the stages apart).
+      // V^T fragments for O^T += V^T P^T: k-step st, element i of lane (d, hh) is
+      // key 16 st + 8 (i / 4) + 4 hh + i % 4 (two transposed reads of 4 keys each).
+      // The address of (st, hl) is the (0, 0) one plus 2048 st + 1024 hl: the
+      // swizzle (fa_v_slot) depends on bit 1 of the row only, which st and hl do
+      // not change, so those steps become the reads' immediate offsets. As
+      // builtins the reads get exact LDS waits (the K/V loads are assembly the
+      // compiler does not count), so it can issue them early and wait only
+      // before the P V MFMAs.
       fa_u32x2 vt[2][4][2];
-      {
-        // The address of (st, hl) is the (0, 0) one plus 2048 st + 1024 hl: the
-        // swizzle (fa_v_slot) depends on bit 1 of the row only, which st and hl
-        // do not change, so those steps are the reads' immediate offsets.
-        const unsigned vb = static_cast<unsigned>(reinterpret_cast<uintptr_t>(vs));
-        unsigned ad[2];
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const int dim = 32 * db + tr_dim;
-          ad[db] = vb + tr_row * 128 + fa_v_slot(tr_row, dim >> 3) * 16 + (dim & 7) * 2;
-        }
-        asm volatile(
-            "ds_read_b64_tr_b16 %0, %16\n\tds_read_b64_tr_b16 %1, %16 offset:1024\n\t"
-            "ds_read_b64_tr_b16 %2, %16 offset:2048\n\tds_read_b64_tr_b16 %3, %16 offset:3072\n\t"
-            "ds_read_b64_tr_b16 %4, %16 offset:4096\n\tds_read_b64_tr_b16 %5, %16 offset:5120\n\t"
-            "ds_read_b64_tr_b16 %6, %16 offset:6144\n\tds_read_b64_tr_b16 %7, %16 offset:7168\n\t"
-            "ds_read_b64_tr_b16 %8, %17\n\tds_read_b64_tr_b16 %9, %17 offset:1024\n\t"
-            "ds_read_b64_tr_b16 %10, %17 offset:2048\n\tds_read_b64_tr_b16 %11, %17 offset:3072\n\t"
-            "ds_read_b64_tr_b16 %12, %17 offset:4096\n\tds_read_b64_tr_b16 %13, %17 offset:5120\n\t"
-            "ds_read_b64_tr_b16 %14, %17 offset:6144\n\tds_read_b64_tr_b16 %15, %17 offset:7168\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(vt[0][0][0]), "=&v"(vt[0][0][1]), "=&v"(vt[0][1][0]), "=&v"(vt[0][1][1]), "=&v"(vt[0][2][0]),
-              "=&v"(vt[0][2][1]), "=&v"(vt[0][3][0]), "=&v"(vt[0][3][1]), "=&v"(vt[1][0][0]), "=&v"(vt[1][0][1]),
-              "=&v"(vt[1][1][0]), "=&v"(vt[1][1][1]), "=&v"(vt[1][2][0]), "=&v"(vt[1][2][1]), "=&v"(vt[1][3][0]),
-              "=&v"(vt[1][3][1])
-            : "v"(ad[0]), "v"(ad[1]));
+      for (int db = 0; db < 2; ++db) {
+        const int dim = 32 * db + tr_dim;
+        const unsigned char* vb = vs + tr_row * 128 + fa_v_slot(tr_row, dim >> 3) * 16 + (dim & 7) * 2;
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int hl = 0; hl < 2; ++hl)
+            vt[db][st][hl] = __builtin_bit_cast(
+                fa_u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                              (__attribute__((address_space(3))) fa_i16x4*)(vb + 2048 * st + 1024 * hl)));
       }
       // Online softmax in the log2 domain with c = scale * log2(e) > 0: the row
       // maximum is taken on the raw scores, p = 2^(s c - m) is one FMA and one
