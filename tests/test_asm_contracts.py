@@ -6,6 +6,11 @@ kernel that uses it, each M0 write must be its own (followed by one wait state,
 s_nop 0, then its buffer_load ... lds), so the compiler never keeps a value of
 its own in M0 there, and no LDS-DMA load directly follows the M0 write it reads
 (GFX9 needs one wait state between the two).
+
+The compiler does not count those loads, so a vmcnt wait it inserts for a
+load of its own also waits for every K/V block in flight. In the prefill
+attention, after the first LDS-DMA load, every vmcnt wait must be one of the
+kernel's own waits right before its barriers.
 """
 
 import re
@@ -72,3 +77,16 @@ def test_m0_written_only_by_load_lds16(src_name):
         assert loads > 0, fname
         assert not any(ins.startswith("global_load_lds") for ins in body), fname
     assert checked > 0, f"no kernel of {KERNELS[src_name]} found in {src_name}"
+
+
+def test_prefill_attention_loop_has_no_compiler_vmcnt_wait():
+    funcs = functions(device_asm("attention.hip"))
+    bodies = [b for name, b in funcs.items() if "attention_prefill_kernel" in name]
+    assert bodies, "attention_prefill_kernel not found"
+    for body in bodies:
+        first = next(i for i, ins in enumerate(body) if ins.startswith("buffer_load_dwordx4") and ins.endswith("lds"))
+        waits = [(i, ins) for i, ins in enumerate(body[first:], first) if ins.startswith("s_waitcnt") and "vmcnt" in ins]
+        assert waits, "no vmcnt wait after the first K/V load"
+        for i, ins in waits:
+            nxt = body[i + 1] if i + 1 < len(body) else ""
+            assert nxt == "s_barrier", (i, ins, nxt)
