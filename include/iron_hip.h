@@ -209,6 +209,18 @@ int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k
                     const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
                     int head_dim, int max_len, int pos, const int* pos_dev, float scale, void* stream);
 
+/* iron_gqa_decode with flags. IRON_GQA_KV_RESIDENT: the caches stay resident
+ * between calls (a decode loop over all layers of a model whose caches fit the
+ * 256 MB Infinity Cache), so the K/V reads are ordinary, allocating loads;
+ * without it (iron_gqa_decode) they are streaming loads, which are faster when
+ * the caches come from HBM on every call. Results are identical either way;
+ * unknown flag bits are rejected (IRON_EINVAL) before anything runs. Same
+ * reference interface as iron_gqa_decode (llama_npu.py:486-523). */
+#define IRON_GQA_KV_RESIDENT 1
+int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                       const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
+                       int head_dim, int max_len, int pos, const int* pos_dev, float scale, int flags, void* stream);
+
 /* iron_gqa_decode without a workspace argument: the counters and partials go
  * to a scratch array the library holds in device memory, one per GPU, for the life of the
  * process (iron_gqa_decode_noalloc_max_bytes(), 4 MiB: at the Llama-3.2-1B

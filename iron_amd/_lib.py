@@ -40,6 +40,7 @@ SIGNATURES: dict[str, list] = {
     "iron_softmax": [_P, _P, _I, _I, _I, _P, _P],
     "iron_rope": [_P, _P, _I, _P, _I, _I, _I, _I, _P],
     "iron_gqa_decode": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P],
+    "iron_gqa_decode_ex": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _P],
     "iron_gqa_decode_noalloc": [_P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _F, _P],
     "iron_attention_prefill": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _LL, _LL, _LL, _LL, _LL, _LL, _I, _I, _I, _F, _P],
     "iron_gemm_bf16_nt": [_P, _P, _P, _I, _I, _I, _LL, _I, _I, _F, _F, _P],

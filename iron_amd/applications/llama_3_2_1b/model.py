@@ -40,6 +40,7 @@ from ... import _lib
 from ...common.graph import capture_graph
 
 BF16 = torch.bfloat16
+KV_RESIDENT = 1  # IRON_GQA_KV_RESIDENT of iron_gqa_decode_ex (include/iron_hip.h)
 
 
 @dataclass
@@ -279,6 +280,12 @@ class LlamaHIP:
         self.angles = compute_rope_angles(Hd, L, cfg.rope_base, cfg.rope_scaling).to(dev)
         ws = _lib.query("iron_gqa_decode_workspace_bytes", cfg.n_heads, cfg.n_kv_groups, Hd, L)
         self.attn_ws = torch.zeros(int(ws), dtype=torch.uint8, device=dev)
+        # The decode step reads every layer's caches once per token while ~1 GB of
+        # weights streams past them: caches that fit well inside the 256 MB
+        # Infinity Cache stay there between steps when the attention reads them
+        # with allocating loads (IRON_GQA_KV_RESIDENT).
+        kv_bytes = 2 * cfg.n_layers * cfg.n_kv_groups * L * Hd * 2
+        self.kv_flags = KV_RESIDENT if kv_bytes <= (192 << 20) else 0
         # decode buffers (fixed addresses: the captured graph refers to them)
         self.x = torch.zeros(E, dtype=BF16, device=dev)
         self.qkv = torch.zeros(cfg.qkv_dim, dtype=BF16, device=dev)
@@ -349,10 +356,10 @@ class LlamaHIP:
         scale = 1.0 / math.sqrt(Hd)
         for i, L in enumerate(self.layers):
             L["qkv"].gemv(self.x, self.qkv, s, norm_scale=True, eps=cfg.eps)
-            _lib.call("iron_gqa_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
+            _lib.call("iron_gqa_decode_ex", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), self.angles.data_ptr(), self.angles.shape[0], self.attn.data_ptr(),
                       self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, 0,
-                      self.pos.data_ptr(), scale, s)
+                      self.pos.data_ptr(), scale, self.kv_flags, s)
             L["o"].gemv(self.attn, self.x, s, residual=self.x)
             L["gate"].gemv(self.x, self.h, s, norm_scale=True, eps=cfg.eps, pair=L["up"])
             L["down"].gemv(self.h, self.x, s, residual=self.x)

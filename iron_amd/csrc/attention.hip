@@ -173,7 +173,7 @@ __device__ __forceinline__ int dec_v_slot(int R, int c) { return c ^ (((R >> 1) 
 template <int G>
 __device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid);
 
-template <int G, bool MERGE>
+template <int G, bool MERGE, bool RES>
 __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int D = kD;
   constexpr int NW = kDecThreads / kWave;
@@ -238,10 +238,15 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     qa[e] = *reinterpret_cast<const float2*>(angrow + 2 * i);
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the q loads ahead of the K/V loads
-  // K rows (clamped: rows >= pos are replaced or masked below)
+  // K rows (clamped: rows >= pos are replaced or masked below). RES: the caches
+  // stay resident between calls (a decode loop over all layers; ~134 MB at 4096
+  // positions fits the Infinity Cache while the weights stream past it), so the
+  // K/V loads are ordinary, allocating loads (decode +0.9%). Otherwise they are
+  // streaming loads, faster when the caches come from HBM every time.
+  auto ld_kv = [](const uint16_t* p) { return RES ? *reinterpret_cast<const uint4*>(p) : ld_stream16(p); };
   const int krow = min(wrow0 + r, a.max_len - 1);
-  uint4 k0 = ld_stream16(a.k_cache + (hb + krow) * D + cq * 8);
-  uint4 k1 = ld_stream16(a.k_cache + (hb + krow) * D + (cq + 4) * 8);
+  uint4 k0 = ld_kv(a.k_cache + (hb + krow) * D + cq * 8);
+  uint4 k1 = ld_kv(a.k_cache + (hb + krow) * D + (cq + 4) * 8);
   // V rows: lane l of load u holds row 8 u + l / 8, 16-byte chunk dec_v_slot(row, l % 8),
   // stored below into slot l % 8 of the wave's LDS block
   unsigned char* vblk = v_s[w];
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
   for (int u = 0; u < 2; ++u) {
     const int R = 8 * u + (lane >> 3);
     const int vrow = min(wrow0 + R, a.max_len - 1);
-    vraw[u] = ld_stream16(a.v_cache + (hb + vrow) * D + dec_v_slot(R, lane & 7) * 8);
+    vraw[u] = ld_kv(a.v_cache + (hb + vrow) * D + dec_v_slot(R, lane & 7) * 8);
   }
 #pragma unroll
   for (int e = 0; e < QN; ++e) {
@@ -1033,10 +1038,24 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
 // aligned); shared by the entry point that takes a workspace (counters kept
 // at zero between calls) and the one that uses the library's own scratch
 // array (clear_counters: zeroed before each call by a small kernel).
+// One launch (n_kv_heads a multiple of 8: each KV head's chunks on one XCD,
+// merged by the last to finish) or the partials kernel plus the merge kernel.
+template <int G, bool RES>
+static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, hipStream_t s) {
+  const dim3 block(kDecThreads);
+  if (n_kv_heads % kXcds == 0) {
+    IRON_LAUNCH((gqa_decode_kernel<G, true, RES>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
+  } else {
+    IRON_LAUNCH((gqa_decode_kernel<G, false, RES>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
+    IRON_LAUNCH((gqa_combine_kernel<G>), dim3(n_kv_heads * G), dim3(kMergeThreads), 0, s, a);
+  }
+}
+
 static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
                              void* v_cache, const float* angles, int angle_rows, void* out, void* workspace,
                              int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
-                             float scale, void* stream, bool clear_counters) {
+                             float scale, void* stream, bool clear_counters, int flags) {
+  IRON_REQUIRE((flags & ~IRON_GQA_KV_RESIDENT) == 0, "%s: unknown flags 0x%x", who, static_cast<unsigned>(flags));
   IRON_REQUIRE(q && k_new && v_new && k_cache && v_cache && angles && out && workspace, "%s: null pointer", who);
   IRON_REQUIRE(head_dim == kD, "%s: head_dim=%d (only 64 is supported)", who, head_dim);
   IRON_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
@@ -1068,36 +1087,22 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.nsplit = decode_nsplit(max_len);
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 block(kDecThreads);
-  if (n_kv_heads % kXcds == 0) {  // one launch: each KV head's chunks on one XCD, merged by the last to finish
-    if (clear_counters) IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
-    const dim3 grid(a.nsplit * n_kv_heads);
+  if (n_kv_heads % kXcds == 0 && clear_counters)
+    IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
+  if (flags & IRON_GQA_KV_RESIDENT) {
     switch (G) {
-      case 1: IRON_LAUNCH((gqa_decode_kernel<1, true>), grid, block, 0, s, a); break;
-      case 2: IRON_LAUNCH((gqa_decode_kernel<2, true>), grid, block, 0, s, a); break;
-      case 4: IRON_LAUNCH((gqa_decode_kernel<4, true>), grid, block, 0, s, a); break;
-      default: IRON_LAUNCH((gqa_decode_kernel<8, true>), grid, block, 0, s, a); break;
+      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, s); break;
+      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, s); break;
+      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, s); break;
+      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, s); break;
     }
-    return check_launch(who);
-  }
-  const dim3 grid(a.nsplit, n_kv_heads), cgrid(n_kv_heads * G), cblock(kMergeThreads);
-  switch (G) {
-    case 1:
-      IRON_LAUNCH((gqa_decode_kernel<1, false>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<1>), cgrid, cblock, 0, s, a);
-      break;
-    case 2:
-      IRON_LAUNCH((gqa_decode_kernel<2, false>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<2>), cgrid, cblock, 0, s, a);
-      break;
-    case 4:
-      IRON_LAUNCH((gqa_decode_kernel<4, false>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<4>), cgrid, cblock, 0, s, a);
-      break;
-    default:
-      IRON_LAUNCH((gqa_decode_kernel<8, false>), grid, block, 0, s, a);
-      IRON_LAUNCH((gqa_combine_kernel<8>), cgrid, cblock, 0, s, a);
-      break;
+  } else {
+    switch (G) {
+      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, s); break;
+      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, s); break;
+      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, s); break;
+      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, s); break;
+    }
   }
   return check_launch(who);
 }
@@ -1107,7 +1112,16 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
                                int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
                                void* stream) {
   return gqa_decode_launch("iron_gqa_decode", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, workspace,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false, 0);
+}
+
+extern "C" int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                                  const float* angles, int angle_rows, void* out, void* workspace, int n_heads,
+                                  int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
+                                  int flags, void* stream) {
+  return gqa_decode_launch("iron_gqa_decode_ex", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out,
+                           workspace, n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false,
+                           flags);
 }
 
 // The workspace of iron_gqa_decode_noalloc: a file-scope device array, one
@@ -1164,7 +1178,7 @@ extern "C" int iron_gqa_decode_noalloc(const void* q, const void* k_new, const v
   void* ws = decode_scratch_ptr("iron_gqa_decode_noalloc");
   if (!ws) return IRON_EINVAL;
   return gqa_decode_launch("iron_gqa_decode_noalloc", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, ws,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, true);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, true, 0);
 }
 
 extern "C" int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads,

@@ -123,3 +123,11 @@ def test_offset_limits_rejected_on_host():
     with pytest.raises(_lib.IronHipError, match="2 GiB"):
         _lib.call("iron_attention_prefill", p, p, p, p, 8, 8, 16, 1 << 20, 64, 64, 512, 64, 1 << 10, 64, 512, 16, 1, 0,
                   0.125, None)
+
+
+def test_gqa_decode_ex_rejects_unknown_flags_on_host():
+    """Flag bits other than IRON_GQA_KV_RESIDENT are refused before anything runs."""
+    from iron_amd import _lib
+
+    with pytest.raises(_lib.IronHipError, match="unknown flags"):
+        _lib.call("iron_gqa_decode_ex", 16, 16, 16, 16, 16, 16, 128, 16, 256, 32, 8, 64, 128, 0, None, 0.125, 2, None)

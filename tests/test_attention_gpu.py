@@ -195,3 +195,30 @@ def test_attention_prefill_abi(gpu, H, Hkv, Sq, Skv, causal, q_offset):
     max_abs, rel_l2 = ops.max_abs_rel_l2(got, ref)
     assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
     assert torch.all(O[Sq:].cpu() == 0)
+
+
+@pytest.mark.parametrize("Hkv", [8, 2])
+@pytest.mark.parametrize("pos", [0, 200, 511])
+def test_gqa_decode_ex_resident_matches(gpu, Hkv, pos):
+    """iron_gqa_decode_ex with IRON_GQA_KV_RESIDENT (allocating K/V loads) gives
+    the bits of iron_gqa_decode (streaming loads): outputs and appended cache
+    rows, on the one-launch path (Hkv 8) and the two-kernel path (Hkv 2)."""
+    from iron_amd import _lib
+
+    H, max_len = 4 * Hkv, 512
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, L=max_len, seed=pos + 21)
+    angles = ops.rope_angles_table(64, max_len).to(gpu)
+    ws_bytes = int(_lib.query("iron_gqa_decode_workspace_bytes", H, Hkv, 64, max_len))
+    results = []
+    for fn, extra in (("iron_gqa_decode", ()), ("iron_gqa_decode_ex", (1,))):
+        qd, knd, vnd = q.to(gpu), kn.to(gpu), vn.to(gpu)
+        kcd, vcd = kc.to(gpu).clone(), vc.to(gpu).clone()
+        out = torch.empty(H, 64, dtype=torch.bfloat16, device=gpu)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=gpu)
+        _lib.call(fn, qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), angles.data_ptr(),
+                  angles.shape[0], out.data_ptr(), ws.data_ptr(), H, Hkv, 64, max_len, pos, None, 0.125, *extra,
+                  _lib.stream_handle(gpu))
+        torch.cuda.synchronize()
+        results.append((out.cpu(), kcd.cpu(), vcd.cpu()))
+    (o0, k0, v0), (o1, k1, v1) = results
+    assert torch.equal(o0, o1) and torch.equal(k0, k1) and torch.equal(v0, v1)
