@@ -40,7 +40,9 @@ def device_asm(src_name):
 
 
 def functions(asm):
-    """name -> list of instruction lines of each function in the assembly."""
+    """name -> list of instruction lines of each function in the assembly (a
+    function runs from its label to its .Lfunc_end label: it may hold several
+    s_endpgm, one per exit)."""
     funcs, name, body = {}, None, []
     for line in asm.splitlines():
         m = re.match(r"^(_Z\S+):", line)
@@ -48,12 +50,13 @@ def functions(asm):
             name, body = m.group(1), []
             funcs[name] = body
             continue
+        if line.startswith(".Lfunc_end"):
+            name = None
+            continue
         if name is not None:
             s = line.split(";")[0].strip()
             if s and not s.startswith("."):
                 body.append(s)
-            if s.startswith("s_endpgm"):
-                name = None
     return funcs
 
 
