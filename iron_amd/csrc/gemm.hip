@@ -13,7 +13,8 @@
 // instantiated and gemm_launch picks one with a cost model: 256x256 (8 waves
 // of 64x128), 256x192 (8 waves of 64x96, when it divides N), 256x128 (8 waves
 // of 64x64), 128x128 with 8 waves of 64x32 (one workgroup per CU, 3 steps of
-// look-ahead) and 128x128 with 4 waves of 64x64 (two workgroups per CU). Bigger tiles fetch fewer bytes per flop: at ~64
+// look-ahead) and 128x128 with 4 waves of 64x64 (two workgroups per CU).
+// Shapes too small to give every CU a 128x128 tile take 64x64 or 128x64 tiles. Bigger tiles fetch fewer bytes per flop: at ~64
 // B/clk of L2->CU fill per CU, a 128x128x64 step needs as many cycles to fill
 // as its MFMAs take, a 256x256 step half as many. Two waves per SIMD hide each
 // other's LDS and barrier waits, which matters most when each CU has a single
@@ -112,6 +113,8 @@ using TileM = Tile<4, 2, 2, 2, 2, true>;   // 256x128, 8 waves of 64x64, 96 KiB
 using TileS = Tile<2, 4, 2, 1, 4>;         // 128x128, 8 waves of 64x32, 128 KiB, 3 steps ahead
 using TileS2 = Tile<2, 2, 2, 2, 2>;        // 128x128, 4 waves of 64x64, 64 KiB: two workgroups per CU
 using TileL3 = Tile<4, 2, 2, 3, 2, true>;  // 256x192, 8 waves of 64x96, 112 KiB: N = 3072 in 16 tiles
+using Tile64 = Tile<2, 2, 1, 1, 4>;        // 64x64, 4 waves of 32x32, 64 KiB: shapes too small for 128x128
+using Tile128x64 = Tile<2, 2, 2, 1, 4>;    // 128x64, 4 waves of 64x32, 96 KiB
 
 // A 16-byte LDS access of 16 lanes covers all 64 banks once when their 16
 // consecutive rows use 16 distinct (row parity, slot) pairs: the slot is
@@ -739,6 +742,21 @@ static void launch_tile_i4(const GemmArgs& a, hipStream_t s) {
 }
 
 static void gemm_launch(const GemmArgs& a, hipStream_t s) {
+  // Shapes whose 128x128 tiles leave CUs idle (with no workspace for a K
+  // split): the smaller tile whose count comes closest to one per CU without
+  // going over. 512 tokens, cold weights: 512x2048 -> 2048 19.7 -> 12.3 us
+  // (64x64), -> 3072 20.0 -> 15.9 us (128x64), 512x8192 -> 2048 65.6 -> 40.5 us
+  // (64x64). The SwiGLU pair needs 128-column tiles.
+  if (a.splits == 1 && a.epi != kEpiSwigluPair && tile_count<TileS>(a) < 256) {
+    if (tile_count<Tile64>(a) <= 256) {
+      launch_tile<Tile64>(a, s);
+      return;
+    }
+    if (tile_count<Tile128x64>(a) <= 256) {
+      launch_tile<Tile128x64>(a, s);
+      return;
+    }
+  }
   const double cl = launch_cost<TileL>(a, 1, 1000.0), cm = launch_cost<TileM>(a, 1, 900.0);
   const double cs = launch_cost<TileS>(a, 1, 660.0), cs2 = launch_cost<TileS2>(a, 2, 800.0);
   // 256x192 only where it divides N exactly (wave quantization: 3968x3072 gets 256 tiles instead of 192 of
