@@ -59,6 +59,7 @@ FLM = [
     (512, 1024, 2048, "silu", (-4.0, 4.0)),
     (1024, 1536, 6144, "none", None),
     (1024, 2560, 10240, "none", None),
+    (1000, 576, 1500, "silu", (-3.0, 3.0)),  # 128x64 tiles, ragged in M and N
 ]
 
 
@@ -78,7 +79,7 @@ def test_flm_gemm(gpu, M, K, N, epilogue, clamp):
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 2048), (512, 2048, 512), (512, 2048, 8192), (512, 8192, 2048),
-                                   (13, 2048, 3072)])
+                                   (13, 2048, 3072), (512, 2048, 3072), (1000, 576, 1500)])
 def test_prefill_gemm_shapes(gpu, M, K, N):
     """Config 5 prefill projections (A activations, B = nn.Linear weight (N, K)), fp32-accumulated
     reference; BASELINE bar max-abs 2e-2 / rel-L2 1e-2 on N(0,1) activations x N(0,0.02^2) weights."""
