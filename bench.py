@@ -2,13 +2,14 @@
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--mode full|gemv|gemv_bf16|model|prefill|gemm_large|attention|floor|mfma]
+                    [--mode full|gemv|gemv_bf16|model|prefill|gemm_large|gemm_512|attention|floor|mfma]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
 runs only the Llama configuration; --mode prefill only the config 5 prefill
 GEMM and the 3968-token causal attention; --mode gemm_large the 3968-token
-prefill projections and 4096^3 beside hipBLASLt; --mode attention the GQA decode
+prefill projections and 4096^3 beside hipBLASLt; --mode gemm_512 the plain
+(no K split) 512-token projections beside hipBLASLt; --mode attention the GQA decode
 attention at config 3 and at KV 4096; --mode floor the per-launch floors (an
 empty kernel as a graph node, a pure streaming read of the decode kernels'
 sizes). The modes exist for kernel traces and counters.
@@ -740,7 +741,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
-    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "gemm_large", "attention", "floor",
+    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "gemm_large", "gemm_512", "attention", "floor",
                                        "mfma"],
                     default="full")
     args = ap.parse_args()
@@ -782,6 +783,12 @@ def main() -> int:
         shapes = {"o_proj_3968": (3968, 2048, 2048), "qkv_3968": (3968, 2048, 3072), "down_3968": (3968, 8192, 2048),
                   "gate_up_3968": (3968, 2048, 16384), "square_4096": (4096, 4096, 4096)}
         return emit("gemm_large", {k: bench_prefill_gemm(torch, lib, tm, dev, 10, shape=v) for k, v in shapes.items()})
+    if args.mode == "gemm_512":
+        # the 512-token projections through the plain entry point (no workspace, so no K split: the smaller tiles
+        # for shapes whose 128x128 tiles leave CUs idle), each beside hipBLASLt on the same shape and weights
+        shapes = {"o_proj_512": (512, 2048, 2048), "qkv_512": (512, 2048, 3072), "down_512": (512, 8192, 2048),
+                  "gate_up_512": (512, 2048, 16384)}
+        return emit("gemm_512", {k: bench_prefill_gemm(torch, lib, tm, dev, 50, shape=v) for k, v in shapes.items()})
     if args.mode == "attention":
         return emit("attention", {
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300),
