@@ -109,7 +109,7 @@ struct Tile {
   static_assert(BM * BN * 2 <= NS * kStage * 16, "the bf16 C tile must fit in the stages' LDS");
 };
 using TileL = Tile<4, 2, 2, 4, 2, true>;   // 256x256, 8 waves of 64x128, 128 KiB
-using TileM = Tile<4, 2, 2, 2, 2, true>;   // 256x128, 8 waves of 64x64, 96 KiB
+using TileM = Tile<4, 2, 2, 2, 3, true>;   // 256x128, 8 waves of 64x64, 3 stages (144 KiB; one workgroup per CU either way)
 using TileS = Tile<2, 4, 2, 1, 4>;         // 128x128, 8 waves of 64x32, 128 KiB, 3 steps ahead
 using TileS2 = Tile<2, 2, 2, 2, 2>;        // 128x128, 4 waves of 64x64, 64 KiB: two workgroups per CU
 using TileL3 = Tile<4, 2, 2, 3, 2, true>;  // 256x192, 8 waves of 64x96, 112 KiB: N = 3072 in 16 tiles
