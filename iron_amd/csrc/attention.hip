@@ -878,7 +878,7 @@ __global__ __launch_bounds__(256) void attention_prefill_kernel(PrefillArgs a) {
     }
     if (!visible(bi)) return;  // every key of the block (and of the next) is after this wave's queries
     fa_bf16x8 kf[2][4];
-    k_frags(bi + 1, kf);  // waited for with the V^T reads below
+    k_frags(bi + 1, kf);  // issued now; the compiler waits for them (exact LDS counts) before their MFMAs
     const int k0 = bi * kFaK;
     const unsigned char* vs = lds + (bi % kFaStages) * 2 * kFaBlock + kFaBlock;
       // V^T fragments for O^T += V^T P^T: k-step st, element i of lane (d, hh) is

@@ -9,14 +9,15 @@
 // operands: C^T = B A^T).
 //
 // Tiles: a workgroup of WMW x WNW waves owns a (WMW*TI*32) x (WNW*TJ*32)
-// output tile; each wave owns TI x TJ MFMA tiles of 32x32. Five shapes are
-// instantiated and gemm_launch picks one with a cost model: 256x256 (8 waves
-// of 64x128), 256x192 (8 waves of 64x96, when it divides N), 256x128 (8 waves
-// of 64x64), 128x128 with 8 waves of 64x32 (one workgroup per CU, 3 steps of
-// look-ahead) and 128x128 with 4 waves of 64x64 (two workgroups per CU).
-// Shapes too small to give every CU a 128x128 tile take 64x64 or 128x64 tiles. Bigger tiles fetch fewer bytes per flop: at ~64
-// B/clk of L2->CU fill per CU, a 128x128x64 step needs as many cycles to fill
-// as its MFMAs take, a 256x256 step half as many. Two waves per SIMD hide each
+// output tile; each wave owns TI x TJ MFMA tiles of 32x32. gemm_launch picks
+// one of five shapes with a cost model: 256x256 (8 waves of 64x128), 256x192
+// (8 waves of 64x96, when it divides N), 256x128 (8 waves of 64x64, 3 stages),
+// 128x128 with 8 waves of 64x32 (one workgroup per CU, 3 steps of look-ahead)
+// and 128x128 with 4 waves of 64x64 (two workgroups per CU). Shapes too small
+// to give every CU a 128x128 tile take 64x64 or 128x64 tiles (4 waves).
+// Bigger tiles fetch fewer bytes per flop: at ~64 B/clk of L2->CU fill per CU,
+// a 128x128x64 step needs as many cycles to fill as its MFMAs take, a 256x256
+// step half as many. Two waves per SIMD hide each
 // other's LDS and barrier waits, which matters most when each CU has a single
 // workgroup.
 //
