@@ -155,8 +155,8 @@ __device__ __forceinline__ int dec_v_slot(int R, int c) { return c ^ (((R >> 1) 
 //                values and two permlane exchanges; fp32 weights in the log2
 //                domain.
 //   O = P V      A = P as bf16 pairs hi + lo (two MFMAs: the weights keep
-//                ~16 bits), B = V^T read from the wave's LDS block (filled by
-//                global_load_lds) with ds_read_b64_tr_b16; lane l (l / 16 <
+//                ~16 bits), B = V^T read from the wave's LDS block (the V rows,
+//                loaded to registers, stored there) with ds_read_b64_tr_b16; lane l (l / 16 <
 //                G / 4) ends with heads 4 (l / 16) + [0, 4) at dims 16 t + l % 16.
 // The new token's k (rotated) and v replace their row (and are appended to
 // the caches); rows past pos are masked (scores) and zeroed (V). The four
@@ -644,9 +644,9 @@ __global__ __launch_bounds__(kWave) void gqa_clear_counters_kernel(unsigned* ctr
 //
 // Workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries and
 // walks the visible keys in blocks of 64. K and V blocks are staged row-major
-// in a 3-stage LDS ring filled by global_load_lds_dwordx4 (no VGPR staging, no
-// LDS stores), two blocks ahead of the one being computed, one barrier per
-// block. Per block a wave computes S^T = K Q^T (two 32x32 tiles): every lane
+// in a 4-stage LDS ring filled by LDS-direct loads (buffer_load_dwordx4 ... lds,
+// load_lds16: no VGPR staging, no LDS stores), up to three blocks ahead of the
+// one being computed, one barrier per block. Per block a wave computes S^T = K Q^T (two 32x32 tiles): every lane
 // then holds one query column (lane % 32) and 16 keys, so the softmax row
 // statistics need only the lane's own registers and one exchange with lane ^ 32.
 // The probabilities go to bf16 and feed O^T += V^T P^T directly from registers

@@ -21,8 +21,8 @@
 // other's LDS and barrier waits, which matters most when each CU has a single
 // workgroup.
 //
-// K advances 64 per step through an NS-stage LDS ring filled by
-// global_load_lds_dwordx4: the loads write LDS directly, with no VGPR staging
+// K advances 64 per step through an NS-stage LDS ring filled by LDS-direct
+// loads (buffer_load_dwordx4 ... lds, load_lds16): they write LDS directly, with no VGPR staging
 // and no ds_write (ds_write_b128 sustains ~73 B/clk per CU against ~205 B/clk
 // for ds_read_b128, and was the main loop's bottleneck). A stage holds the A
 // rows then the B rows, 128 B (64 bf16) each, in 1 KiB blocks of 8 rows; the
