@@ -397,6 +397,68 @@ int iron_qkv_rope_scatter_splitk(const float* partial, int splits, const float* 
                                  void* k_cache, void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim,
                                  int max_len, int pos0, void* stream);
 
+/* ------------------------------------------ One-launch decode step ---- */
+
+/* Per-layer device pointers of the one-launch decode step (a device array of
+ * n_layers of these): int4-group-32 signed codes (N, K/2) and bf16 scales
+ * (N, K/32) of qkv (3072 x 2048, input_layernorm folded in), o (2048 x 2048),
+ * gate and up (8192 x 2048, post_attention_layernorm folded in), down
+ * (2048 x 8192), and the layer's K/V caches (8, max_len, 64) bf16. */
+typedef struct IronDecodeLayer {
+  const void* qkv_codes;
+  const void* qkv_scales;
+  const void* o_codes;
+  const void* o_scales;
+  const void* gate_codes;
+  const void* gate_scales;
+  const void* up_codes;
+  const void* up_scales;
+  const void* down_codes;
+  const void* down_scales;
+  void* k_cache;
+  void* v_cache;
+} IronDecodeLayer;
+
+/* Bytes of the exchange area of iron_llama_decode_fused for n_layers (-1 if
+ * invalid). */
+long long iron_llama_decode_fused_exchange_bytes(int n_layers);
+
+/* One decode step of a Llama-3.2-1B-shaped model (hidden 2048, 32 query / 8
+ * KV heads of 64, FFN 8192, int4-g32 linears) in ONE launch, up to the final
+ * hidden state: the token selection of iron_argmax_select (keys of the
+ * previous head; token, history[*pos], *pos += 1, embedding), then per layer
+ * the qkv GEMV (rms scale), the GQA attention of iron_gqa_decode_ex (RoPE,
+ * cache append at the new position), o_proj + residual, the SwiGLU pair and
+ * down + residual; x_out (2048 bf16) receives the last layer's output.
+ * Results are bit-identical to those 82 separate launches. Stages hand their
+ * vectors over inside the launch through `exchange`
+ * (iron_llama_decode_fused_exchange_bytes, 256-byte aligned, zero-filled once;
+ * contents carry over between calls) tagged with *epoch, which must be
+ * nonzero and must change between calls: iron_llama_decode_head advances it.
+ * attn_workspace: iron_gqa_decode_workspace_bytes(32, 8, 64, max_len), its
+ * counters zero (the kernel leaves them at zero). max_len: a multiple of 64.
+ * Every wait inside the launch is bounded by wait_us microseconds: on
+ * timeout the launch still ends and *status (device word, zero before the
+ * call) becomes nonzero (bits: 1 layer input, 2 position, 4 q/k/v, 8
+ * attention output, 16 o_proj output, 32 h, 64 a residual); a nonzero
+ * *status also makes every later wait give up at once. flags:
+ * IRON_GQA_KV_RESIDENT. Replaces the single fused decode dispatch of
+ * iron/applications/llama_3.2_1b/llama_npu.py:459-584 (its runlist minus
+ * the LM head). */
+int iron_llama_decode_fused(const IronDecodeLayer* layers, int n_layers, const void* keys, int n_keys,
+                            const void* embed, int vocab, int* token, int* pos, int* history, int history_cap,
+                            const float* angles, int angle_rows, int max_len, float scale, float eps,
+                            void* attn_workspace, void* exchange, void* x_out, const unsigned* epoch,
+                            unsigned* status, unsigned wait_us, int flags, void* stream);
+
+/* The LM head that ends a one-launch decode step: logits = W' x *
+ * rsqrt(mean(x^2) + eps) with argmax keys (iron_gemv_bf16_fused with W, or
+ * iron_gemv_i4g32_fused with signed codes/scales, norm_mode 2), and *epoch
+ * advanced by one (0 skipped) for the next step's exchange tags. Same
+ * reference step as those two (llama_npu.py:559-584). */
+int iron_llama_decode_head(const void* W, const void* codes, const void* scales, const void* x, void* logits, int M,
+                           int K, float eps, void* argmax_keys, unsigned* epoch, void* stream);
+
 /* -------------------------------------------------- Measurement probes ---- */
 /* No counterpart in the reference: they measure the floors that bound the
  * short decode kernels (bench.py --mode floor). */

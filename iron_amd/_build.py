@@ -49,7 +49,11 @@ HIP_FLAGS = [
 # accumulators in AGPRs the compiler copied them back and forth every block.
 # -fno-honor-nans: max(a, b) of finite scores then needs no NaN-quieting
 # v_max_f32 per operand (finite inputs give identical results).
-FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"]}
+# decode_fused.hip runs the same decode attention body, so it takes the same flags.
+FILE_FLAGS = {
+    "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+    "decode_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+}
 
 
 def _hipcc() -> str:

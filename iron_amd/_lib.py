@@ -59,6 +59,9 @@ SIGNATURES: dict[str, list] = {
     "iron_qkv_rope_scatter_splitk": [_P, _I, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P],
     "iron_rmsnorm_splitk": [_P, _P, _I, _P, _P, _P, _I, _I, _F, _P],
     "iron_gemm_nt_partials": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _LL, _P],
+    "iron_llama_decode_fused": [_P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _I, _F, _F, _P, _P, _P, _P, _P,
+                                ctypes.c_uint, _I, _P],
+    "iron_llama_decode_head": [_P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P],
     "iron_probe_empty": [_I, _P],
     "iron_probe_read": [_P, _LL, _P, _LL, _I, _P],
     "iron_probe_mfma": [_I, _I, _I, _I, _P, _P, _LL, _P],
@@ -69,6 +72,7 @@ SIGNATURES: dict[str, list] = {
 QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
     "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
+    "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
     "iron_probe_read_workgroups": (_LL, [_LL, _I]),

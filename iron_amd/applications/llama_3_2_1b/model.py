@@ -69,6 +69,11 @@ class LlamaConfig:
     # (RoPE scatter, RMSNorm), which merges them: one launch fewer per split
     # GEMM, bit-identical results
     prefill_fuse_merge: bool = True
+    # decode step as one launch (iron_llama_decode_fused) plus the head, for the
+    # Llama-3.2-1B shape with int4 linears; otherwise (or False) 82 launches
+    decode_fused: bool = False
+    # bound on every wait inside the one-launch step (microseconds)
+    decode_wait_us: int = 200000
 
     @property
     def head_dim(self) -> int:
@@ -299,6 +304,22 @@ class LlamaHIP:
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.history = torch.zeros(L, dtype=torch.int32, device=dev)
         self.host_pos = 0
+        # The one-launch decode step (Llama-3.2-1B shape, int4 linears): a device
+        # table of per-layer pointers (IronDecodeLayer), the exchange area, the
+        # epoch its tags carry and the status word its bounded waits report to.
+        self.fused = bool(cfg.decode_fused and cfg.int4 and cfg.emb_dim == 2048 and cfg.hidden_dim == 8192
+                          and cfg.n_heads == 32 and cfg.n_kv_groups == 8 and cfg.max_seq_len % 64 == 0)
+        if self.fused:
+            table = []
+            for i, Ly in enumerate(self.layers):
+                for name in ("qkv", "o", "gate", "up", "down"):
+                    table += [Ly[name].codes.data_ptr(), Ly[name].scales.data_ptr()]
+                table += [self.k_cache[i].data_ptr(), self.v_cache[i].data_ptr()]
+            self.layer_table = torch.tensor(table, dtype=torch.int64).to(dev)
+            nbytes = int(_lib.query("iron_llama_decode_fused_exchange_bytes", cfg.n_layers))
+            self.exchange = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+            self.epoch = torch.ones(1, dtype=torch.int32, device=dev)
+            self.status = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph = None
         self.graph_multi = None
         self._prefill_bufs = None  # activations of the longest prompt seen (see _pbufs)
@@ -347,6 +368,18 @@ class LlamaHIP:
         (pos advances), then the layers, then the head writes logits and keys."""
         cfg, s = self.cfg, self._stream()
         Hd, q_rows, kv_rows = cfg.head_dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
+        if self.fused:
+            _lib.call("iron_llama_decode_fused", self.layer_table.data_ptr(), cfg.n_layers, self.keys.data_ptr(),
+                      self.n_keys, self.embed.data_ptr(), cfg.vocab_size, self.token.data_ptr(), self.pos.data_ptr(),
+                      self.history.data_ptr(), cfg.max_seq_len, self.angles.data_ptr(), self.angles.shape[0],
+                      cfg.max_seq_len, 1.0 / math.sqrt(Hd), cfg.eps, self.attn_ws.data_ptr(),
+                      self.exchange.data_ptr(), self.x.data_ptr(), self.epoch.data_ptr(), self.status.data_ptr(),
+                      cfg.decode_wait_us, self.kv_flags, s)
+            h = self.head
+            _lib.call("iron_llama_decode_head", _lib.ptr(None if h.int4 else h.bf16), _lib.ptr(h.codes if h.int4 else None),
+                      _lib.ptr(h.scales if h.int4 else None), self.x.data_ptr(), self.logits.data_ptr(), h.N, h.K,
+                      cfg.eps, self.keys.data_ptr(), self.epoch.data_ptr(), s)
+            return
         _lib.call("iron_argmax_select", self.keys.data_ptr(), self.n_keys, self.embed.data_ptr(), cfg.emb_dim,
                   cfg.vocab_size, self.x.data_ptr(), self.token.data_ptr(), self.pos.data_ptr(),
                   self.history.data_ptr(), cfg.max_seq_len, s)
@@ -364,6 +397,20 @@ class LlamaHIP:
             L["gate"].gemv(self.x, self.h, s, norm_scale=True, eps=cfg.eps, pair=L["up"])
             L["down"].gemv(self.h, self.x, s, residual=self.x)
         self.head.gemv(self.x, self.logits, s, norm_scale=True, eps=cfg.eps, keys=self.keys)
+
+    def check_decode_status(self) -> None:
+        """Raise if a wait inside a one-launch decode step gave up (waits for the
+        stream). The status word is cleared, so later steps can run again."""
+        if not self.fused:
+            return
+        st = int(self.status.item())
+        if st:
+            # a step that gave up can leave attention arrival counters part-way
+            self.attn_ws.zero_()
+            self.status.zero_()
+            torch.cuda.synchronize(self.device)
+            raise RuntimeError(f"one-launch decode step: a wait gave up (status 0x{st:x}; bits: 1 layer input, "
+                               "2 position, 4 q/k/v, 8 attention output, 16 o_proj output, 32 h, 64 residual)")
 
     def commit(self) -> None:
         """Record the token chosen by the last logits (history[pos], pos += 1)
@@ -386,6 +433,7 @@ class LlamaHIP:
         self.pos.copy_(pos)
         self.keys.copy_(keys)
         torch.cuda.synchronize(self.device)
+        self.check_decode_status()
 
     # decode steps per replay of the multi-step graph: fewer graph launches per token
     # (measured at KV 3968 -> 4096: 457.9 us/token with one step per graph, 454.0 with 4, 453.6 with 8)
@@ -419,6 +467,7 @@ class LlamaHIP:
             else:
                 self.decode_step()
         self.host_pos += n_steps
+        self.check_decode_status()
 
     # ------------------------------------------------------------ prefill
     def _drop_prefill_graphs(self) -> None:

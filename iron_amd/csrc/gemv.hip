@@ -44,6 +44,7 @@ struct GemvArgs {
   float eps;
   int epi;
   int xcd;  // 1: XCD-contiguous row order (xcd_block)
+  unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
 };
 
 // Normalises the 8 bf16 values of an x chunk: bf16(x * inv * w).
@@ -116,10 +117,21 @@ __device__ __forceinline__ int xcd_block(int enable) {
   return (!enable || (nb & 7)) ? b : (b & 7) * (nb >> 3) + (b >> 3);
 }
 
+// The epoch word of the one-launch decode step (its exchange tags) moves on
+// once per step; the head GEMV that ends the step does it, after every
+// workgroup of the step's launch has read the old value.
+__device__ __forceinline__ void advance_epoch(unsigned* epoch) {
+  if (epoch && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    const unsigned e = *epoch + 1u;
+    *epoch = e ? e : 1u;
+  }
+}
+
 // Fast path: K == 512*U exactly; each lane holds U chunks of W (and W2) in
 // flight. One wave per output row.
 template <int U, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
+  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int tile = xcd_block(a.xcd);
   const int row = tile * 4 + (threadIdx.x >> 6);
@@ -180,6 +192,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
 // Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mode) {
+  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int tile = xcd_block(a.xcd);
   const int row = tile * 4 + (threadIdx.x >> 6);
@@ -282,6 +295,7 @@ struct I4Args {
   uint32_t magic;  // 0x43084308 signed two's-complement nibbles, 0x43004300 unsigned
   float offset;    // 136 signed, 128 unsigned
   int xcd;         // 1: XCD-contiguous row order (xcd_block)
+  unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
 };
 
 // Fast path: K == 2048*GPL*KS. The 4 waves of a workgroup form 4/KS row
@@ -290,6 +304,7 @@ struct I4Args {
 // wave share the x preparation.
 template <int GPL, int R, int KS, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
+  advance_epoch(a.epoch);
   static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int tile = xcd_block(a.xcd);
@@ -442,6 +457,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 // Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) {
+  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool active = row < a.M;
@@ -705,6 +721,29 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
            1};  // XCD-contiguous rows: measured faster for every int4 shape of the decode step
   hipStream_t s = static_cast<hipStream_t>(stream);
   return codes2 ? launch_gemv_i4<true>(a, norm_mode, s) : launch_gemv_i4<false>(a, norm_mode, s);
+}
+
+extern "C" int iron_llama_decode_head(const void* W, const void* codes, const void* scales, const void* x,
+                                      void* logits, int M, int K, float eps, void* argmax_keys, unsigned* epoch,
+                                      void* stream) {
+  IRON_REQUIRE((W != nullptr) != (codes != nullptr), "iron_llama_decode_head: give W (bf16) or codes (int4), not both");
+  IRON_REQUIRE(x && logits && argmax_keys && epoch, "iron_llama_decode_head: null pointer");
+  IRON_REQUIRE(M > 0 && K > 0 && K % 32 == 0, "iron_llama_decode_head: M=%d K=%d (K must be a multiple of 32)", M, K);
+  IRON_REQUIRE(aligned16(x) && (!W || aligned16(W)) && (!codes || (aligned16(codes) && scales)),
+               "iron_llama_decode_head: operands must be 16-byte aligned (int4 needs its scales)");
+  IRON_REQUIRE(logits != x, "iron_llama_decode_head: logits must not alias x");
+  IRON_REQUIRE((reinterpret_cast<uintptr_t>(argmax_keys) & 7u) == 0 && (reinterpret_cast<uintptr_t>(epoch) & 3u) == 0,
+               "iron_llama_decode_head: keys must be 8-byte and epoch 4-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (W) {
+    GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x), static_cast<uint16_t*>(logits),
+               nullptr, nullptr, static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, 0, epoch};
+    return launch_gemv_bf16<false>(a, NORM_SCALE, 1, s);
+  }
+  I4Args a{static_cast<const uint8_t*>(codes), static_cast<const uint16_t*>(scales), nullptr, nullptr,
+           static_cast<const uint16_t*>(x), static_cast<uint16_t*>(logits), nullptr, nullptr,
+           static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, 0x43084308u, 136.f, 1, epoch};
+  return launch_gemv_i4<false>(a, NORM_SCALE, s);
 }
 
 extern "C" int iron_dequant_i4(const void* codes, const void* scales, void* out, int N, int K, int group,
