@@ -440,7 +440,7 @@ long long iron_llama_decode_fused_exchange_bytes(int n_layers);
  * Every wait inside the launch is bounded by wait_us microseconds: on
  * timeout the launch still ends and *status (device word, zero before the
  * call) becomes nonzero (bits: 1 layer input, 2 position, 4 q/k/v, 8
- * attention output, 16 o_proj output, 32 h, 64 a residual); a nonzero
+ * attention output, 16 o_proj output, 32 h); a nonzero
  * *status also makes every later wait give up at once. flags:
  * IRON_GQA_KV_RESIDENT. Replaces the single fused decode dispatch of
  * iron/applications/llama_3.2_1b/llama_npu.py:459-584 (its runlist minus

@@ -410,7 +410,7 @@ class LlamaHIP:
             self.status.zero_()
             torch.cuda.synchronize(self.device)
             raise RuntimeError(f"one-launch decode step: a wait gave up (status 0x{st:x}; bits: 1 layer input, "
-                               "2 position, 4 q/k/v, 8 attention output, 16 o_proj output, 32 h, 64 residual)")
+                               "2 position, 4 q/k/v, 8 attention output, 16 o_proj output, 32 h)")
 
     def commit(self) -> None:
         """Record the token chosen by the last logits (history[pos], pos += 1)

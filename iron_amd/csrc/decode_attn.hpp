@@ -191,9 +191,9 @@ struct DecodeKv {
   uint4 k0, k1, v0, v1;
 };
 template <bool RES>
-__device__ __forceinline__ DecodeKv load_kv_rows(const uint16_t* k_cache, const uint16_t* v_cache, int max_len,
-                                                 int s, int j) {
-  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x >> 6;
+__device__ __forceinline__ DecodeKv load_kv_rows(int tid, const uint16_t* k_cache, const uint16_t* v_cache,
+                                                 int max_len, int s, int j) {
+  const int lane = tid & (kWave - 1), w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, cq = lane >> 4;
   const int wrow0 = s * kDecChunk + 16 * w;
   const size_t hb = static_cast<size_t>(j) * max_len;
@@ -214,6 +214,7 @@ __device__ __forceinline__ DecodeKv load_kv_rows(const uint16_t* k_cache, const 
 template <int G>
 struct PlainDecodeIo {
   static constexpr bool kEarly = true;
+  static constexpr int kMergeLoads = 16;
   const DecodeArgs& a;
   __device__ __forceinline__ void new_kv(int j, int cq, uint4& kna, uint4& knb, uint4& vna, uint4& vnb) const {
     kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * kD + cq * 8);
@@ -227,9 +228,10 @@ struct PlainDecodeIo {
     qp = qh[t ^ 32];
   }
   __device__ __forceinline__ bool wait_inputs(int) const { return true; }
+  __device__ __forceinline__ int thread() const { return threadIdx.x; }
   template <bool RES>
   __device__ __forceinline__ DecodeKv kv_rows(const DecodeArgs& d, int s, int j) const {
-    return load_kv_rows<RES>(d.k_cache, d.v_cache, d.max_len, s, j);
+    return load_kv_rows<RES>(threadIdx.x, d.k_cache, d.v_cache, d.max_len, s, j);
   }
   __device__ __forceinline__ void store_out(size_t off, uint32_t lo, uint32_t hi) const {
     *reinterpret_cast<uint2*>(a.out + off) = make_uint2(lo, hi);
@@ -249,7 +251,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   __shared__ __attribute__((aligned(16))) float wo_s[NW][G * D];
   __shared__ __attribute__((aligned(16))) unsigned char v_s[NW][16 * 128];  // each wave's 16 V rows
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid >> 6;
+  const int tid = io.thread(), lane = tid & (kWave - 1), w = tid >> 6;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * kDecChunk;
@@ -498,7 +500,7 @@ __device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid, const
     return *reinterpret_cast<const float4*>(base + static_cast<size_t>(min(c0 + q + NQ * b, nact - 1)) * PS + 4 * qd);
   };
   // one batch with N (<= 16) output loads per thread per round
-  auto batch = [&](auto n_tag, int c0) {
+  auto batch = [&](auto n_tag, int c0, bool one_round) {
     constexpr int N = decltype(n_tag)::value;
     float st_m[NE], st_l[NE];
 #pragma unroll
@@ -565,18 +567,21 @@ __device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid, const
         acc.w = fmaf(wv[b], ob[b].w, acc.w);
       }
       if (N < PER && b0 + N >= PER) break;
-      if (N < 16) break;  // a short batch takes one round
+      if (one_round) break;  // the batch covered the slice's live chunks
     }
     __syncthreads();  // w_s and sc_s are rewritten by the next batch
   };
   for (int c0 = 0; c0 < nact; c0 += CB) {
     const int span = (min(CB, nact - c0) + NQ - 1) / NQ;  // live chunks per slice (uniform)
+    // Io::kMergeLoads caps the output loads in flight per thread (registers);
+    // a capped batch takes as many rounds as the slice needs
+    constexpr int NMAX = PER < Io::kMergeLoads ? PER : Io::kMergeLoads;
     if (span <= 4 && PER >= 4)
-      batch(std::integral_constant<int, (PER < 4 ? PER : 4)>{}, c0);
-    else if (span <= 8 && PER >= 8)
-      batch(std::integral_constant<int, 8>{}, c0);
+      batch(std::integral_constant<int, (PER < 4 ? PER : 4)>{}, c0, true);
+    else if (span <= 8 && NMAX >= 8)
+      batch(std::integral_constant<int, 8>{}, c0, true);
     else
-      batch(std::integral_constant<int, (PER < 16 ? PER : 16)>{}, c0);
+      batch(std::integral_constant<int, NMAX>{}, c0, NMAX < 16 && NMAX >= span);
   }
   oo_s[tid] = acc;
   __syncthreads();

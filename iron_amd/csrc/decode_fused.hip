@@ -48,13 +48,6 @@ constexpr int kF = 8192;                         // FFN size
 constexpr int kNH = 32, kNKV = 8, kGQ = 4;       // query heads, KV heads, heads per KV head
 constexpr int kQKV = (kNH + 2 * kNKV) * kD;      // 3072 q|k|v rows
 
-// Workgroups per stage (256 threads each)
-constexpr int kWgSel = 8;         // the select workgroup, padded to one per XCD
-constexpr int kWgQkv = kQKV / 4;  // one row per wave
-constexpr int kWgO = kE / 4;      // one row per wave
-constexpr int kWgPair = kF / 8;   // two gate and two up rows per wave
-constexpr int kWgDown = kE / 8;   // two rows (K = 8192) per wave
-
 // Exchange area in 8-byte pairs: the position pair, then per layer its input
 // x, qkv, attention output, x after o_proj, h; the last layer's output x
 // follows the last layer.
@@ -78,7 +71,6 @@ enum : unsigned {
   kStAtt = 8u,   // o_proj: attention output
   kStX1 = 16u,   // gate/up: x after o_proj
   kStH = 32u,    // down: h
-  kStRes = 64u,  // a residual
 };
 
 struct FusedArgs {
@@ -129,6 +121,16 @@ __device__ __forceinline__ void st_pair(__amdgpu_buffer_rsrc_t r, int p, uint32_
   __builtin_amdgcn_raw_buffer_store_b64(u32x2_v{d, tag}, r, p * 8, 0, kSc1);
 }
 
+// threadIdx.x as a value the compiler must treat as new at every call: the
+// persistent loop then recomputes each thread-dependent address where it is
+// used instead of hoisting dozens of them out of the loop and keeping them
+// live (which spilled registers).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ unsigned long long now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 __device__ __forceinline__ unsigned read_status(const unsigned* status) {
   return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -139,28 +141,22 @@ __device__ __forceinline__ void give_up(unsigned* status, unsigned bit) {
 // Workgroup barrier for LDS only: the weight and cache loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// XCD-contiguous tile of local workgroup b of a stage of nb workgroups (stage
-// starts are multiples of 8, so b % 8 is the XCD): each XCD owns one
-// contiguous run of tiles.
-__device__ __forceinline__ int stage_tile(int b, int nb) { return (b & 7) * (nb >> 3) + (b >> 3); }
-// The last pair written by the last workgroup on XCD x of a GEMV stage (pw pairs per workgroup).
-__device__ __forceinline__ int gemv_sentinel(int x, int nb, int pw) { return (x * (nb >> 3) + (nb >> 3) - 1) * pw + pw - 1; }
-
 // Waits until pairs [p0, p0 + NP) carry `tag` and leaves their data words in
-// dst[0, NP) (LDS). Lanes 0-7 of wave 0 first poll sent[x] (relative to p0),
+// dst[0, NP) (LDS). Lanes x = 0-7 of wave 0 first poll pair sent_a x + sent_b
+// (relative to p0: the last pair of the last producer on XCD x),
 // lane 8 the status word; then every thread loads its share once and re-polls
 // only pairs still missing. Whole workgroup (flag: two LDS words); false,
 // for every thread alike, when it gave up.
 template <int NP>
-__device__ bool wait_vector(__amdgpu_buffer_rsrc_t r, unsigned* status, int p0, const int* sent, unsigned tag,
-                            unsigned limit, unsigned bit, uint32_t* dst, int* flag) {
+__device__ bool wait_vector(__amdgpu_buffer_rsrc_t r, unsigned* status, int p0, int sent_a, int sent_b,
+                            unsigned tag, unsigned limit, unsigned bit, uint32_t* dst, int* flag) {
   static_assert(NP % 512 == 0, "two pairs per 16-byte load, 256 threads");
-  const int tid = threadIdx.x;
+  const int tid = opaque_tid();
   if (tid < kWave) {
     const unsigned long long t0 = now_ticks();
     int fail = 0;
     for (;;) {
-      const u32x2_v v = ld_pair(r, p0 + sent[tid & 7]);
+      const u32x2_v v = ld_pair(r, p0 + sent_a * (tid & 7) + sent_b);
       const unsigned st = tid == 8 ? read_status(status) : 0u;
       if (__builtin_amdgcn_ballot_w64(st != 0u)) {
         fail = 1;
@@ -184,22 +180,26 @@ __device__ bool wait_vector(__amdgpu_buffer_rsrc_t r, unsigned* status, int p0, 
     if (f == 2 && tid == 0) give_up(status, bit);
     return false;
   }
-  constexpr int NL = NP / 512;
-  u32x4_v v[NL];
-#pragma unroll
-  for (int i = 0; i < NL; ++i) v[i] = ld_pairs2(r, p0 + 2 * (tid + 256 * i));
+  constexpr int NL = NP / 512;         // 16-byte loads per thread
+  constexpr int NB = NL < 4 ? NL : 4;  // in flight at once (registers)
   bool ok = true;
 #pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    if (v[i][1] != tag || v[i][3] != tag) {  // rare: re-poll this pair of pairs
-      const unsigned long long t0 = now_ticks();
-      while (ok && (v[i][1] != tag || v[i][3] != tag)) {
-        if (read_status(status) != 0u || now_ticks() - t0 > limit) ok = false;
-        __builtin_amdgcn_s_sleep(1);
-        v[i] = ld_pairs2(r, p0 + 2 * (tid + 256 * i));
+  for (int i0 = 0; i0 < NL; i0 += NB) {
+    u32x4_v v[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) v[i] = ld_pairs2(r, p0 + 2 * (tid + 256 * (i0 + i)));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if (v[i][1] != tag || v[i][3] != tag) {  // rare: re-poll this pair of pairs
+        const unsigned long long t0 = now_ticks();
+        while (ok && (v[i][1] != tag || v[i][3] != tag)) {
+          if (read_status(status) != 0u || now_ticks() - t0 > limit) ok = false;
+          __builtin_amdgcn_s_sleep(1);
+          v[i] = ld_pairs2(r, p0 + 2 * (tid + 256 * (i0 + i)));
+        }
       }
+      *reinterpret_cast<uint2*>(dst + 2 * (tid + 256 * (i0 + i))) = make_uint2(v[i][0], v[i][2]);
     }
-    *reinterpret_cast<uint2*>(dst + 2 * (tid + 256 * i)) = make_uint2(v[i][0], v[i][2]);
   }
   if (!ok) {
     give_up(status, bit);
@@ -209,159 +209,158 @@ __device__ bool wait_vector(__amdgpu_buffer_rsrc_t r, unsigned* status, int p0, 
   return flag[1] == 0;
 }
 
-// The data word of pair p (a residual: rows 2p, 2p + 1), polled by the whole
-// wave. The pair is complete by the time a stage needs it (the stage's input
-// depends on it), so the wait is a guard: if it gives up, the status records
-// it and the caller goes on with whatever it read (the step has failed; every
-// wave still reaches the workgroup's barriers).
-__device__ __forceinline__ uint32_t wait_pair(__amdgpu_buffer_rsrc_t r, unsigned* status, int p, unsigned tag,
-                                              unsigned limit) {
-  u32x2_v v = ld_pair(r, p);
-  if (v[1] != tag) {
+// Waits (wave 0, lanes x = 0-7: pair p0 + sa x) until the 8 sentinel pairs
+// carry `tag`, without loading the vector: a point in time, not data. Whole
+// workgroup; false, for every thread alike, when it gave up.
+__device__ bool wait_seen(__amdgpu_buffer_rsrc_t r, unsigned* status, int p0, int sa, unsigned tag, unsigned limit,
+                          unsigned bit, int* flag) {
+  const int tid = opaque_tid();
+  if (tid < kWave) {
     const unsigned long long t0 = now_ticks();
-    while (v[1] != tag) {
-      const unsigned s = read_status(status);
-      if (s != 0u || now_ticks() - t0 > limit) {
-        if (s == 0u) give_up(status, kStRes);
+    int fail = 0;
+    for (;;) {
+      const u32x2_v v = ld_pair(r, p0 + sa * (tid & 7));
+      const unsigned st = tid == 8 ? read_status(status) : 0u;
+      if (__builtin_amdgcn_ballot_w64(st != 0u)) {
+        fail = 1;
+        break;
+      }
+      if (!__builtin_amdgcn_ballot_w64(tid < 8 && v[1] != tag)) break;
+      if (now_ticks() - t0 > limit) {
+        fail = 2;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
-      v = ld_pair(r, p);
     }
+    if (tid == 0) flag[0] = fail;
   }
-  return v[0];
+  lds_barrier();
+  const int f = flag[0];
+  if (f == 2 && tid == 0) give_up(status, bit);
+  return f == 0;
 }
 
-// A GEMV stage's workgroup: rows (tile * 4 + wave) * R + [0, R) of an int4
-// group-32 matrix (K = 2048 * GPL), the arithmetic of gemv_i4_fast<GPL, R, 1,
-// PAIR, NM> (signed codes, no epilogue). Input: the KP-pair vector at in_p0;
-// residual: the pairs at res_p0; output: pairs at out_p0 (+ plain bf16 copy).
-template <int GPL, int R, bool PAIR, int NM, bool RESID>
-__device__ void gemv_role(const FusedArgs& a, int tile, const uint8_t* codes, const uint16_t* scales,
-                          const uint8_t* codes2, const uint16_t* scales2, int in_p0, const int* sent, unsigned in_bit,
-                          int res_p0, int out_p0, uint16_t* plain, unsigned tag, uint32_t* xs, int* flag) {
-  constexpr int G = GPL * kWave;   // groups per row
-  constexpr int K = G * 32;
-  constexpr int KP = K / 2;        // input pairs
+// int4 group-32 GEMV rows held in registers: the codes (16-byte chunks, lane
+// l owning groups l + 64 j) and scales of R rows of one or (PAIR) two
+// matrices, K = 2048 * GPL.
+template <int GPL, int R, bool PAIR>
+struct GemvRegs {
+  uint4 c[R][GPL];
+  uint4 c2[PAIR ? R : 1][GPL];
+  uint16_t s[R][GPL];
+  uint16_t s2[PAIR ? R : 1][GPL];
+};
+
+// Issues the loads of rows row0 .. row0 + R - 1 (streaming: each weight byte is read once per step).
+template <int GPL, int R, bool PAIR>
+__device__ __forceinline__ void gemv_fetch(GemvRegs<GPL, R, PAIR>& w, const void* codes, const void* scales,
+                                           const void* codes2, const void* scales2, int row0) {
+  constexpr int G = GPL * kWave;
   constexpr size_t crow = static_cast<size_t>(G) * 16;
+  const int lane = opaque_tid() & (kWave - 1);
+  // the rows are the wave's (uniform): their bases stay in scalar registers and
+  // each lane adds only its own 32-bit offset
+  const int row = __builtin_amdgcn_readfirstlane(row0);
+  const uint8_t* c = static_cast<const uint8_t*>(codes) + static_cast<size_t>(row) * crow;
+  const uint8_t* c2 = static_cast<const uint8_t*>(codes2) + static_cast<size_t>(row) * crow;
+  const uint16_t* sc = static_cast<const uint16_t*>(scales) + static_cast<size_t>(row) * G;
+  const uint16_t* sc2 = static_cast<const uint16_t*>(scales2) + static_cast<size_t>(row) * G;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const unsigned off = static_cast<unsigned>(r * crow) + static_cast<unsigned>(lane + j * kWave) * 16u;
+      w.c[r][j] = ld_stream16(c + off);
+      if (PAIR) w.c2[r][j] = ld_stream16(c2 + off);
+    }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < GPL; ++j) {
+      const unsigned off = static_cast<unsigned>(r * G + lane + j * kWave);
+      w.s[r][j] = sc[off];
+      if (PAIR) w.s2[r][j] = sc2[off];
+    }
+}
+
+// The R row values (bf16 bits) of the rows in w against the K-vector in xs
+// (LDS), the arithmetic of gemv_i4_fast<GPL, R, 1, PAIR, NM> for signed
+// codes: the same group products, per-row accumulation order over the groups,
+// DPP totals, norm scale, SiLU and residual. The groups are taken one at a
+// time (each row still sums them in order), which keeps fewer registers live.
+template <int GPL, int R, bool PAIR, int NM, bool RESID>
+__device__ __forceinline__ void gemv_rows(const GemvRegs<GPL, R, PAIR>& w, const uint32_t* xs, float eps,
+                                          const float (&rres)[R], uint16_t (&out)[R]) {
+  constexpr int K = GPL * kWave * 32;
   constexpr uint32_t kMagic = 0x43084308u;  // signed codes
   constexpr float kOffset = 136.f;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int row0 = (tile * 4 + wave) * R;
-  const int g0 = lane;
-
-  // The weights first: nothing of this step is needed to fetch them.
-  uint4 cw[R][GPL], cw2[R][GPL];
-  uint16_t sc[R][GPL], sc2[R][GPL];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const size_t row = static_cast<size_t>(row0 + r);
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = g0 + j * kWave;
-      cw[r][j] = ld_stream16(codes + row * crow + static_cast<size_t>(g) * 16);
-      if (PAIR) cw2[r][j] = ld_stream16(codes2 + row * crow + static_cast<size_t>(g) * 16);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const size_t row = static_cast<size_t>(row0 + r);
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const int g = g0 + j * kWave;
-      sc[r][j] = scales[row * G + g];
-      if (PAIR) sc2[r][j] = scales2[row * G + g];
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  const __amdgpu_buffer_rsrc_t xr_ = xch_rsrc(a.xch);
-  if (!wait_vector<KP>(xr_, a.status, in_p0, sent, tag, a.wait_ticks, in_bit, xs, flag)) return;
-  float rres[R];
-  if (RESID) {
-    const uint32_t d = wait_pair(xr_, a.status, res_p0 + (row0 >> 1), tag, a.wait_ticks);
-    if (R == 2) {
-      rres[0] = lo_bf16(d);
-      if (R > 1) rres[R - 1] = hi_bf16(d);
-    } else {
-      rres[0] = (row0 & 1) ? hi_bf16(d) : lo_bf16(d);
-    }
-  }
-
-  uint4 xrv[GPL][4];
+  const int lane = opaque_tid() & (kWave - 1);
   const uint4* xv = reinterpret_cast<const uint4*>(xs);
+  float acc[R], acc2[R], ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < GPL; ++j)
+  for (int r = 0; r < R; ++r) acc[r] = acc2[r] = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xrv[j][q] = xv[(g0 + j * kWave) * 4 + q];
-  float inv = 1.f;
-  if (NM == NORM_SCALE) {
-    float ss = 0.f;
+  for (int j = 0; j < GPL; ++j) {
+    uint4 xr[4];
 #pragma unroll
-    for (int j = 0; j < GPL; ++j)
+    for (int q = 0; q < 4; ++q) xr[q] = xv[(lane + j * kWave) * 4 + q];
+    if (NM == NORM_SCALE) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xrv[j][q], ss);
-    ss = wave_sum(ss);
-    inv = inv_rms(ss, K, a.eps);
+      for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xr[q], ss);
+    }
+    XGroup xg;
+    build_xgroup(xr, xg);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      acc[r] = fmaf(bf16_to_f32(w.s[r][j]), i4_group_total(w.c[r][j], xg, kMagic, kOffset), acc[r]);
+      if (PAIR) acc2[r] = fmaf(bf16_to_f32(w.s2[r][j]), i4_group_total(w.c2[r][j], xg, kMagic, kOffset), acc2[r]);
+    }
   }
-  XGroup xg[GPL];
-#pragma unroll
-  for (int j = 0; j < GPL; ++j) build_xgroup(xrv[j], xg[j]);
-  uint16_t outv[R];
+  const float inv = NM == NORM_SCALE ? inv_rms(wave_sum(ss), K, eps) : 1.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float acc = 0.f, acc2 = 0.f;
-#pragma unroll
-    for (int j = 0; j < GPL; ++j) {
-      const float d = i4_group_total(cw[r][j], xg[j], kMagic, kOffset);
-      acc = fmaf(bf16_to_f32(sc[r][j]), d, acc);
-      if (PAIR) {
-        const float d2 = i4_group_total(cw2[r][j], xg[j], kMagic, kOffset);
-        acc2 = fmaf(bf16_to_f32(sc2[r][j]), d2, acc2);
-      }
-    }
-    float t = wave_sum(acc);
-    float t2 = PAIR ? wave_sum(acc2) : 0.f;
+    float t = wave_sum(acc[r]);
+    float t2 = PAIR ? wave_sum(acc2[r]) : 0.f;
     if (NM == NORM_SCALE) {
       t *= inv;
       t2 *= inv;
     }
     float v = PAIR ? silu_f32(t) * t2 : t;
     if (RESID) v += rres[r];
-    outv[r] = f32_to_bf16(v);
+    out[r] = f32_to_bf16(v);
   }
-  if (R == 2) {
-    if (lane == 0) {
-      const uint32_t d = static_cast<uint32_t>(outv[0]) | (static_cast<uint32_t>(outv[R - 1]) << 16);
-      st_pair(xr_, out_p0 + (row0 >> 1), d, tag);
-      if (plain) *reinterpret_cast<uint32_t*>(plain + row0) = d;
-    }
-  } else {  // four rows of the workgroup: one 16-byte store
-    __shared__ uint16_t rows_s[4];
-    if (lane == 0) rows_s[wave] = outv[0];
-    lds_barrier();
-    if (tid == 0) {
-      const uint32_t d0 = rows_s[0] | (static_cast<uint32_t>(rows_s[1]) << 16);
-      const uint32_t d1 = rows_s[2] | (static_cast<uint32_t>(rows_s[3]) << 16);
-      st_pairs2(xr_, out_p0 + tile * 2, d0, d1, tag);
-      if (plain) *reinterpret_cast<uint2*>(plain + tile * 4) = make_uint2(d0, d1);
-    }
+}
+
+// Publishes one bf16 row per wave, rows 4 t + wave: the four meet in LDS and
+// go out as two pairs in one 16-byte store at pair p0 + 2 t.
+__device__ __forceinline__ void publish_rows4(__amdgpu_buffer_rsrc_t r, int p0, int t, uint16_t v, unsigned tag,
+                                              uint16_t* rows_s) {
+  const int tid = opaque_tid(), lane = tid & (kWave - 1), wave = tid >> 6;
+  if (lane == 0) rows_s[wave] = v;
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    const uint32_t d0 = rows_s[0] | (static_cast<uint32_t>(rows_s[1]) << 16);
+    const uint32_t d1 = rows_s[2] | (static_cast<uint32_t>(rows_s[3]) << 16);
+    st_pairs2(r, p0 + 2 * t, d0, d1, tag);
   }
 }
 
 // The attention's Io inside the step: q (4 heads), k_new and v_new of KV head j
 // are waited for in the exchange area and staged in LDS (st[0..255] q,
-// [256..319] k, [320..383] v as bf16); the merged output is published as pairs.
+// [256..319] k, [320..383] v as bf16); the K/V cache rows were loaded ahead
+// (kv); the merged output is published as pairs.
 struct FusedDecodeIo {
   static constexpr bool kEarly = false;
+  static constexpr int kMergeLoads = 8;  // the persistent workgroup holds other stages' weights too
   const FusedArgs& fa;
   int qkv_p0, att_p0;
   unsigned tag;
   uint32_t* st;  // 192 words of LDS
   int* flag;
+  DecodeKv kv;
   __device__ __forceinline__ bool wait_inputs(int j) const {
     const __amdgpu_buffer_rsrc_t r = xch_rsrc(fa.xch);
-    const int tid = threadIdx.x;
+    const int tid = opaque_tid();
     if (tid == 0) flag[2] = 0;
     lds_barrier();
     if (tid < 96) {  // 192 pairs, two per thread: q (64 loads), k (16), v (16)
@@ -387,82 +386,27 @@ struct FusedDecodeIo {
     lds_barrier();
     return flag[2] == 0;
   }
+  __device__ __forceinline__ int thread() const { return opaque_tid(); }
   __device__ __forceinline__ void q_pair(int, int t, uint16_t& qx, uint16_t& qp) const {
     const uint16_t* q = reinterpret_cast<const uint16_t*>(st);
     qx = q[t];
     qp = q[t ^ 32];
   }
   __device__ __forceinline__ void new_kv(int, int cq, uint4& kna, uint4& knb, uint4& vna, uint4& vnb) const {
-    const uint4* kv = reinterpret_cast<const uint4*>(st + kGQ * kD / 2);  // k at 16-byte chunk 0.., v at 8..
-    kna = kv[cq];
-    knb = kv[cq + 4];
-    vna = kv[8 + cq];
-    vnb = kv[8 + cq + 4];
+    const uint4* kvn = reinterpret_cast<const uint4*>(st + kGQ * kD / 2);  // k at 16-byte chunk 0.., v at 8..
+    kna = kvn[cq];
+    knb = kvn[cq + 4];
+    vna = kvn[8 + cq];
+    vnb = kvn[8 + cq + 4];
   }
   template <bool RES>
-  __device__ __forceinline__ DecodeKv kv_rows(const DecodeArgs& d, int s, int j) const {
-    return load_kv_rows<RES>(d.k_cache, d.v_cache, d.max_len, s, j);
+  __device__ __forceinline__ DecodeKv kv_rows(const DecodeArgs&, int, int) const {
+    return kv;
   }
   __device__ __forceinline__ void store_out(size_t off, uint32_t lo, uint32_t hi) const {
     st_pairs2(xch_rsrc(fa.xch), att_p0 + static_cast<int>(off >> 1), lo, hi, tag);
   }
 };
-
-template <bool RES>
-__device__ void attention_role(const FusedArgs& a, const IronDecodeLayer& L, int n, int lbase, unsigned tag,
-                               uint32_t* st, int* flag) {
-  const int j = n % kXcds, s = n / kXcds;  // all chunks of KV head j on one XCD
-  const __amdgpu_buffer_rsrc_t r = xch_rsrc(a.xch);
-  // the position (published by the select workgroup at the start of the step),
-  // polled by wave 0 and shared through LDS so that every wave takes the same path
-  if (threadIdx.x < kWave) {
-    u32x2_v pv = ld_pair(r, 0);
-    int got = 1;
-    if (pv[1] != tag) {
-      const unsigned long long t0 = now_ticks();
-      while (pv[1] != tag) {
-        const unsigned sv = read_status(a.status);
-        if (sv != 0u || now_ticks() - t0 > a.wait_ticks) {
-          if (sv == 0u && threadIdx.x == 0) give_up(a.status, kStPos);
-          got = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-        pv = ld_pair(r, 0);
-      }
-    }
-    if (threadIdx.x == 0) {
-      flag[0] = got;
-      flag[1] = static_cast<int>(pv[0]);
-    }
-  }
-  lds_barrier();
-  if (!flag[0]) return;
-  const int pos = flag[1];
-  if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) {
-    // never for a position the host accepted; publish zeros so the step drains
-    if (s == 0 && threadIdx.x < kGQ * kD / 4)
-      st_pairs2(r, lbase + kOffAtt + j * (kGQ * kD / 2) + 2 * threadIdx.x, 0u, 0u, tag);
-    return;
-  }
-  DecodeArgs d;
-  d.q = d.k_new = d.v_new = nullptr;
-  d.k_cache = static_cast<uint16_t*>(L.k_cache);
-  d.v_cache = static_cast<uint16_t*>(L.v_cache);
-  d.angles = a.angles;
-  d.out = nullptr;
-  d.part = a.part;
-  d.ctr = a.ctr;
-  d.head_stride = a.head_stride;
-  d.pos_dev = nullptr;
-  d.pos = pos;
-  d.max_len = a.max_len;
-  d.angle_rows = a.angle_rows;
-  d.nsplit = a.nsplit;
-  d.scale_log2 = a.scale_log2;
-  FusedDecodeIo io{a, lbase + kOffQkv, lbase + kOffAtt, tag, st, flag};
-  gqa_decode_chunk<kGQ, true, RES>(d, s, j, pos, io);
-}
 
 // Token selection (the previous head's argmax keys), bookkeeping, and the
 // embedding row as layer 0's input: select_embed_kernel's work by 256 threads,
@@ -504,71 +448,249 @@ __device__ void select_role(const FusedArgs& a, unsigned tag) {
   st_pairs2(r, layer_pairs(0) + 4 * threadIdx.x + 2, v.z, v.w, tag);
 }
 
+// The position of this step (pair 0, published by the select), polled by wave
+// 0 and shared through LDS so that every wave takes the same path; -1 when the
+// wait gave up.
+__device__ int wait_position(const FusedArgs& a, unsigned tag, int* flag) {
+  if (threadIdx.x < kWave) {
+    const __amdgpu_buffer_rsrc_t r = xch_rsrc(a.xch);
+    u32x2_v pv = ld_pair(r, 0);
+    int got = 1;
+    if (pv[1] != tag) {
+      const unsigned long long t0 = now_ticks();
+      while (pv[1] != tag) {
+        const unsigned sv = read_status(a.status);
+        if (sv != 0u || now_ticks() - t0 > a.wait_ticks) {
+          if (sv == 0u && threadIdx.x == 0) give_up(a.status, kStPos);
+          got = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        pv = ld_pair(r, 0);
+      }
+    }
+    if (threadIdx.x == 0) flag[3] = got ? static_cast<int>(pv[0] & 0x7fffffffu) : -1;
+  }
+  lds_barrier();
+  return flag[3];
+}
+
+// The persistent grid: kGrid workgroups, all resident at once (4 per CU), each
+// looping over the layers with a fixed share of every stage:
+//   workgroups [0, kWgA): wave 4 w + v owns qkv row 4 w + v; the workgroup owns
+//     attention chunk w / 8 of KV head w % 8 (w < 8 nsplit) and o rows 4 w + v
+//     (w < 512); and two gate/up rows.
+//   workgroups [kWgA, kGrid): two gate/up rows per wave and two down rows per
+//     wave (K = 8192).
+// Weights are loaded into registers well before their stage: the next layer's
+// qkv row and K/V rows once the current gate/up stage's input has arrived,
+// the o and gate/up rows right after the attention, and on the down
+// workgroups the next layer's gate/up and down rows right after the down
+// stage. None is held through the attention (its registers), and each is
+// issued after a wait, so the next wait for the exchange (loads count in
+// order) finds it long landed.
+constexpr int kGrid = 1024;
+constexpr int kWgA = 768;
+constexpr int kWgOrows = 512;  // workgroups with o rows
+
+template <bool RES>
+__device__ void loop_a(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag) {
+  __shared__ uint16_t rows_s[4];
+  const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gw = w * 4 + wave;
+  const bool has_att = w < kNKV * a.nsplit, has_o = w < kWgOrows;
+  const int j = w % kXcds, s = w / kXcds;  // the attention chunk: all chunks of head j on one XCD
+  const __amdgpu_buffer_rsrc_t xr = xch_rsrc(a.xch);
+  const float none[1] = {0.f};
+
+  GemvRegs<1, 1, false> wq, wo;
+  GemvRegs<1, 2, true> wp;
+  DecodeKv kv{};
+  if (w == 0) select_role(a, tag);  // first: layer 0 waits for it
+  const IronDecodeLayer& L0 = a.layers[0];
+  gemv_fetch(wq, L0.qkv_codes, L0.qkv_scales, nullptr, nullptr, gw);
+  int pos = 0;
+  bool att = false;
+  if (has_att) {
+    pos = wait_position(a, tag, flag);
+    if (pos < 0) return;
+    att = s * kDecChunk <= pos && pos < a.max_len && pos < a.angle_rows;
+    if (att) kv = load_kv_rows<RES>(opaque_tid(), static_cast<const uint16_t*>(L0.k_cache), static_cast<const uint16_t*>(L0.v_cache),
+                                    a.max_len, s, j);
+  }
+  for (int l = 0; l < a.n_layers; ++l) {
+    const IronDecodeLayer& L = a.layers[l];
+    const int base = layer_pairs(l);
+    const bool more = l + 1 < a.n_layers;
+    // qkv = Wqkv' x * rms(x). Sentinels: layer 0's x comes from the select
+    // alone; later ones from the down rows of workgroups kGrid - 8 + x
+    // (pairs 4 (w - kWgA) + 3).
+    const int sa = l == 0 ? 0 : 4, sb = l == 0 ? kE / 2 - 1 : 4 * (kGrid - kWgA - 8) + 3;
+    if (!wait_vector<kE / 2>(xr, a.status, base, sa, sb, tag, a.wait_ticks, kStX, xs, flag)) return;
+    // the o row's residual is x itself: taken from the LDS copy now
+    const float o_res = bf16_to_f32(reinterpret_cast<const uint16_t*>(xs)[gw & (kE - 1)]);
+    {
+      uint16_t v[1];
+      gemv_rows<1, 1, false, NORM_SCALE, false>(wq, xs, a.eps, none, v);
+      publish_rows4(xr, base + kOffQkv, w, v[0], tag, rows_s);
+    }
+    // attention chunk (a position past the cache publishes zeros from chunk 0;
+    // the host never asks for one)
+    if (has_att) {
+      if (pos >= a.max_len || pos >= a.angle_rows) {
+        const int t = opaque_tid();
+        if (s == 0 && t < kGQ * kD / 4) st_pairs2(xr, base + kOffAtt + j * (kGQ * kD / 2) + 2 * t, 0u, 0u, tag);
+      } else if (att) {
+        DecodeArgs d;
+        d.q = d.k_new = d.v_new = nullptr;
+        d.k_cache = static_cast<uint16_t*>(L.k_cache);
+        d.v_cache = static_cast<uint16_t*>(L.v_cache);
+        d.angles = a.angles;
+        d.out = nullptr;
+        d.part = a.part;
+        d.ctr = a.ctr;
+        d.head_stride = a.head_stride;
+        d.pos_dev = nullptr;
+        d.pos = pos;
+        d.max_len = a.max_len;
+        d.angle_rows = a.angle_rows;
+        d.nsplit = a.nsplit;
+        d.scale_log2 = a.scale_log2;
+        FusedDecodeIo io{a, base + kOffQkv, base + kOffAtt, tag, xs, flag, kv};
+        gqa_decode_chunk<kGQ, true, RES>(d, s, j, pos, io);  // always reaches its input wait (flag[2])
+        lds_barrier();
+        if (flag[2]) return;  // that wait gave up (the status says so)
+      }
+    }
+    // this layer's o and gate/up rows: loaded after the attention (not held
+    // through it), ahead of the o stage's wait
+    if (has_o) gemv_fetch(wo, L.o_codes, L.o_scales, nullptr, nullptr, gw);
+    gemv_fetch(wp, L.gate_codes, L.gate_scales, L.up_codes, L.up_scales, 2 * gw);
+    // x1 = x + Wo attn. Sentinels: the last pair of each KV head's merged output.
+    if (has_o) {
+      if (!wait_vector<kNH * kD / 2>(xr, a.status, base + kOffAtt, kGQ * kD / 2, kGQ * kD / 2 - 1, tag, a.wait_ticks,
+                                     kStAtt, xs, flag))
+        return;
+      const float rres[1] = {o_res};
+      uint16_t v[1];
+      gemv_rows<1, 1, false, NORM_NONE, true>(wo, xs, a.eps, rres, v);
+      publish_rows4(xr, base + kOffX1, w, v[0], tag, rows_s);
+    }
+    // h = silu(Wg' x1 * rms) * (Wu' x1 * rms). Sentinels: the o rows of
+    // workgroups kWgOrows - 8 + x (pairs 2 w + 1). The next layer's qkv row and
+    // K/V rows are loaded once x1 is here.
+    if (!wait_vector<kE / 2>(xr, a.status, base + kOffX1, 2, 2 * (kWgOrows - 8) + 1, tag, a.wait_ticks, kStX1, xs,
+                             flag))
+      return;
+    if (more) {
+      const IronDecodeLayer& N = a.layers[l + 1];
+      gemv_fetch(wq, N.qkv_codes, N.qkv_scales, nullptr, nullptr, gw);
+      if (att)
+        kv = load_kv_rows<RES>(opaque_tid(), static_cast<const uint16_t*>(N.k_cache), static_cast<const uint16_t*>(N.v_cache),
+                               a.max_len, s, j);
+    }
+    {
+      uint16_t v[2];
+      gemv_rows<1, 2, true, NORM_SCALE, false>(wp, xs, a.eps, {0.f, 0.f}, v);
+      if ((opaque_tid() & (kWave - 1)) == 0) st_pair(xr, base + kOffH + gw, v[0] | (static_cast<uint32_t>(v[1]) << 16), tag);
+    }
+    lds_barrier();  // every wave is done with xs before the next stage overwrites it
+  }
+}
+
+template <bool RES>
+__device__ void loop_b(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag) {
+  const int w = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int gw = w * 4 + wave;
+  const int drow = 8 * (w - kWgA) + 2 * wave;  // this wave's two down rows
+  const __amdgpu_buffer_rsrc_t xr = xch_rsrc(a.xch);
+  GemvRegs<1, 2, true> wp;
+  GemvRegs<4, 2, false> wd;
+  const IronDecodeLayer& L0 = a.layers[0];
+  gemv_fetch(wp, L0.gate_codes, L0.gate_scales, L0.up_codes, L0.up_scales, 2 * gw);
+  gemv_fetch(wd, L0.down_codes, L0.down_scales, nullptr, nullptr, drow);
+  for (int l = 0; l < a.n_layers; ++l) {
+    const int base = layer_pairs(l);
+    const bool more = l + 1 < a.n_layers;
+    if (!wait_vector<kE / 2>(xr, a.status, base + kOffX1, 2, 2 * (kWgOrows - 8) + 1, tag, a.wait_ticks, kStX1, xs,
+                             flag))
+      return;
+    // the down rows' residual is x1 itself: taken from the LDS copy now
+    const uint32_t d_res = xs[drow >> 1];
+    {
+      uint16_t v[2];
+      gemv_rows<1, 2, true, NORM_SCALE, false>(wp, xs, a.eps, {0.f, 0.f}, v);
+      if ((opaque_tid() & (kWave - 1)) == 0) st_pair(xr, base + kOffH + gw, v[0] | (static_cast<uint32_t>(v[1]) << 16), tag);
+    }
+    lds_barrier();  // xs is rewritten by the next wait
+    // x' = x1 + Wd h. Sentinels: the gate/up rows of workgroups kGrid - 8 + x (pairs 4 w + 3).
+    if (!wait_vector<kF / 2>(xr, a.status, base + kOffH, 4, 4 * (kGrid - 8) + 3, tag, a.wait_ticks, kStH, xs, flag))
+      return;
+    {
+      const float rres[2] = {lo_bf16(d_res), hi_bf16(d_res)};
+      uint16_t v[2];
+      gemv_rows<4, 2, false, NORM_NONE, true>(wd, xs, a.eps, rres, v);
+      const uint32_t out = v[0] | (static_cast<uint32_t>(v[1]) << 16);
+      if ((opaque_tid() & (kWave - 1)) == 0) {
+        st_pair(xr, layer_pairs(l + 1) + (drow >> 1), out, tag);
+        if (!more) *reinterpret_cast<uint32_t*>(a.x_out + drow) = out;
+      }
+    }
+    // The next layer's rows, needed from its gate/up stage on (about a layer
+    // away): issued once that layer's input x is out (its qkv workgroups have
+    // it), so their 28 MB do not queue ahead of that handoff.
+    if (more) {
+      if (!wait_seen(xr, a.status, layer_pairs(l + 1) + 4 * (kGrid - kWgA - 8) + 3, 4, tag, a.wait_ticks, kStX, flag))
+        return;
+      const IronDecodeLayer& N = a.layers[l + 1];
+      gemv_fetch(wp, N.gate_codes, N.gate_scales, N.up_codes, N.up_scales, 2 * gw);
+      gemv_fetch(wd, N.down_codes, N.down_scales, nullptr, nullptr, drow);
+    }
+    lds_barrier();
+  }
+}
+
 // RES: the attention's K/V loads are allocating loads (IRON_GQA_KV_RESIDENT).
 template <bool RES>
-__global__ __launch_bounds__(256) void decode_step_kernel(FusedArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void decode_step_kernel(FusedArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t xs[kF / 2];  // a stage's input vector
   __shared__ int flag[4];
   const unsigned tag = *a.epoch;
-  const int b = blockIdx.x;
-  if (b < kWgSel) {
-    if (b == 0) select_role(a, tag);
-    return;
-  }
-  const int per = kWgQkv + kNKV * a.nsplit + kWgO + kWgPair + kWgDown;
-  const int l = (b - kWgSel) / per;
-  int r = (b - kWgSel) % per;
-  const IronDecodeLayer L = a.layers[l];
-  const int base = layer_pairs(l);
-  int sent[8];
-  if (r < kWgQkv) {  // qkv = Wqkv' x * rms(x); input from the select (layer 0) or the previous down
-#pragma unroll
-    for (int x = 0; x < 8; ++x) sent[x] = l == 0 ? kE / 2 - 1 : gemv_sentinel(x, kWgDown, 4);
-    gemv_role<1, 1, false, NORM_SCALE, false>(a, stage_tile(r, kWgQkv), static_cast<const uint8_t*>(L.qkv_codes),
-                                              static_cast<const uint16_t*>(L.qkv_scales), nullptr, nullptr, base,
-                                              sent, kStX, 0, base + kOffQkv, nullptr, tag, xs, flag);
-    return;
-  }
-  r -= kWgQkv;
-  if (r < kNKV * a.nsplit) {
-    attention_role<RES>(a, L, r, base, tag, xs, flag);
-    return;
-  }
-  r -= kNKV * a.nsplit;
-  if (r < kWgO) {  // x1 = x + Wo attn
-#pragma unroll
-    for (int x = 0; x < 8; ++x) sent[x] = x * (kGQ * kD / 2) + kGQ * kD / 2 - 1;
-    gemv_role<1, 1, false, NORM_NONE, true>(a, stage_tile(r, kWgO), static_cast<const uint8_t*>(L.o_codes),
-                                            static_cast<const uint16_t*>(L.o_scales), nullptr, nullptr,
-                                            base + kOffAtt, sent, kStAtt, base, base + kOffX1, nullptr, tag, xs,
-                                            flag);
-    return;
-  }
-  r -= kWgO;
-  if (r < kWgPair) {  // h = silu(Wg' x1 * rms) * (Wu' x1 * rms)
-#pragma unroll
-    for (int x = 0; x < 8; ++x) sent[x] = gemv_sentinel(x, kWgO, 2);
-    gemv_role<1, 2, true, NORM_SCALE, false>(a, stage_tile(r, kWgPair), static_cast<const uint8_t*>(L.gate_codes),
-                                             static_cast<const uint16_t*>(L.gate_scales),
-                                             static_cast<const uint8_t*>(L.up_codes),
-                                             static_cast<const uint16_t*>(L.up_scales), base + kOffX1, sent, kStX1, 0,
-                                             base + kOffH, nullptr, tag, xs, flag);
-    return;
-  }
-  r -= kWgPair;
-  // x' = x1 + Wd h (the next layer's input; the last layer also writes x_out)
-#pragma unroll
-  for (int x = 0; x < 8; ++x) sent[x] = gemv_sentinel(x, kWgPair, 4);
-  gemv_role<4, 2, false, NORM_NONE, true>(a, stage_tile(r, kWgDown), static_cast<const uint8_t*>(L.down_codes),
-                                          static_cast<const uint16_t*>(L.down_scales), nullptr, nullptr, base + kOffH,
-                                          sent, kStH, base + kOffX1, layer_pairs(l + 1),
-                                          l == a.n_layers - 1 ? a.x_out : nullptr, tag, xs, flag);
+  if (blockIdx.x < kWgA)
+    loop_a<RES>(a, tag, xs, flag);
+  else
+    loop_b<RES>(a, tag, xs, flag);
 }
 
 }  // namespace
 }  // namespace iron
 
 using namespace iron;
+
+#include <mutex>
+
+// The persistent grid needs kGrid workgroups resident at once: at least 256
+// CUs holding 4 of them each (occupancy from the compiled kernel's registers
+// and LDS). Checked once per device and kernel variant.
+static int check_residency(const char* who, bool res) {
+  static std::mutex m;
+  static int known[64][2];  // 0 unknown, 1 fits, -1 does not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail_einval("%s: no current device", who);
+  std::lock_guard<std::mutex> lock(m);
+  int& k = known[dev][res ? 1 : 0];
+  if (k == 0) {
+    int cus = 0, per_cu = 0;
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const hipError_t e = res ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<true>, 256, 0)
+                             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<false>, 256, 0);
+    k = (e == hipSuccess && static_cast<long long>(cus) * per_cu >= kGrid) ? 1 : -1;
+    if (k < 0)
+      return fail_einval("%s: the device holds %d x %d workgroups of this kernel at once, fewer than its %d", who, cus,
+                         per_cu, kGrid);
+  }
+  return k > 0 ? 0 : fail_einval("%s: the device cannot hold the %d workgroups of this kernel at once", who, kGrid);
+}
 
 extern "C" long long iron_llama_decode_fused_exchange_bytes(int n_layers) {
   if (n_layers <= 0 || n_layers > 1024) return -1;
@@ -624,10 +746,11 @@ extern "C" int iron_llama_decode_fused(const IronDecodeLayer* layers, int n_laye
   a.epoch = epoch;
   a.status = status;
   a.wait_ticks = wait_us * 100u;
-  const long long per = kWgQkv + static_cast<long long>(kNKV) * a.nsplit + kWgO + kWgPair + kWgDown;
-  const long long grid = kWgSel + per * n_layers;
-  IRON_REQUIRE(grid < (1LL << 31), "%s: grid too large", who);
-  const dim3 g(static_cast<unsigned>(grid)), blk(256);
+  IRON_REQUIRE(kNKV * a.nsplit <= kWgA, "%s: max_len=%d exceeds %d (one attention chunk per workgroup)", who, max_len,
+               kWgA / kNKV * kDecChunk);
+  // every workgroup waits for others: the whole grid must be resident at once
+  if (int rc = check_residency(who, (flags & IRON_GQA_KV_RESIDENT) != 0)) return rc;
+  const dim3 g(kGrid), blk(256);
   if (flags & IRON_GQA_KV_RESIDENT)
     IRON_LAUNCH(decode_step_kernel<true>, g, blk, 0, static_cast<hipStream_t>(stream), a);
   else
