@@ -38,14 +38,20 @@ depend on K. Other configs: a graph of a multiple of `copies` launches (>= a
 few hundred), replayed untimed then timed; per-launch time = timed replay / n,
 median of 5.
 
-``roofline``: algorithmic bytes / that per-launch device time. ``traffic``: HBM
-bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE, each scaled by the
-counter's reading for a copy of known size.
+``roofline``: algorithmic bytes / the headline kernel's average duration in
+rocprofv3's kernel trace of this command (profiles/gemv_i4g32_cfg2_kernel_trace.md,
+read at run time; each traced dispatch carries its own completion signal, so
+that duration is longer than the untraced per-launch time of ``value``, which
+the line also carries as ``kernel_us_live`` / ``frac_live``). ``traffic``: HBM
+bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE of the same command,
+each scaled by the counter's reading for a copy of known size
+(profiles/gemv_i4g32_cfg2_pmc.md, read at run time).
 ``cpu_baseline``: the CPU oracle (torch: dequantise, then fp32 matvec) timed
-on the host cores on a bounded sample; ``cpu_baseline.model_decode`` times the
-oracle's fp32 Llama forward (greedy decode, Llama-3.2-1B shape) the same way.
-Each config in ``extra`` carries its own ``cpu_baseline`` (configs 1, 3, 4 and
-the config 5 prefill GEMM), in the GPU figure's unit, with the core count.
+on the host cores on a bounded sample; ``cpu_baseline.model_decode`` and
+``extra.llama_cfg5.cpu_baseline`` time the oracle's fp32 Llama forward
+(Llama-3.2-1B shape) at config 5's windows: the 512-token prefill, decode
+after it, and decode at KV 3968 on. Each config in ``extra`` carries its own
+``cpu_baseline`` in the GPU figure's unit, with the core count.
 ``extra`` carries the other BASELINE configurations: bf16 GEMV (cfg 1), GQA
 decode (cfg 3, and at KV 4096), SwiGLU block bf16 and int4 (cfg 4), the
 prefill GEMM with cold weights and the Llama-3.2-1B-shaped model (cfg 5:
@@ -76,10 +82,26 @@ POOL_BYTES = 640 << 20  # rotate through > 512 MiB of distinct weights
 
 METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 
-# HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE +
-# WRITE_SIZE, each scaled by the counter's reading for a copy of known size
-# (profiles/gemv_i4g32_cfg2_pmc.md).
-TRAFFIC_BYTES = 9551390
+# The headline kernel's rocprofv3 evidence, committed under profiles/ and read
+# at run time (each file carries one `bench.py reads: <key> <value>` line):
+# the kernel-trace average duration of the headline command's dispatches,
+# and the HBM bytes per launch from its FETCH_SIZE + WRITE_SIZE passes (each
+# scaled by the counter's reading for a copy of known size).
+TRACE_PROFILE = "profiles/gemv_i4g32_cfg2_kernel_trace.md"
+PMC_PROFILE = "profiles/gemv_i4g32_cfg2_pmc.md"
+
+
+def profile_value(rel_path: str, key: str):
+    """The number on the `bench.py reads: <key> <value>` line of a committed
+    profile summary, or None when the file or the line is missing."""
+    import re
+
+    try:
+        text = (ROOT / rel_path).read_text()
+    except OSError:
+        return None
+    m = re.search(r"bench\.py reads: " + re.escape(key) + r" ([0-9.]+)", text)
+    return float(m.group(1)) if m else None
 
 
 def copies_for(nbytes: int) -> int:
@@ -472,7 +494,7 @@ def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0, shape=(512
     return res
 
 
-def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
+def bench_prefill_attention(torch, lib, tm, dev, n, S=3968, cpu_s=0.0):
     """Causal GQA prefill attention of cfg 5's long prompt (32/8 heads, d 64):
     useful flops 4 * S * (S + 1) / 2 * d per head (QK^T and PV, visible keys).
     The 24 MB of operands are re-read many times per launch by design, so they
@@ -494,7 +516,20 @@ def bench_prefill_attention(torch, lib, tm, dev, n, S=3968):
     for i in range(5):
         launch(i, stream)
     t = tm.rotating_us(launch, 1, n)
-    res = _gpu_line("prefill_attention", t, flops=4.0 * S * (S + 1) / 2 * D * H)
+    flops = 4.0 * S * (S + 1) / 2 * D * H
+    cpu = None
+    if cpu_s > 0:
+        from oracle import ops
+
+        # the oracle takes the whole causal attention of the prompt (all 32 heads);
+        # its value counts the same useful flops as the GPU figure
+        Qc = q.cpu().view(S, H, D).transpose(0, 1).contiguous()
+        Kc, Vc = k.cpu(), v.cpu()
+        cpu = _cpu_line(torch, lambda: ops.attention_reference(Qc, Kc, Vc, causal=True, scale=0.125), cpu_s,
+                        flops / 1e12, "TFLOP/s",
+                        f"causal GQA prefill attention, {S} tokens, 32/8 heads via oracle.ops.attention_reference "
+                        "(torch CPU, fp32 scores and softmax; counted as the GPU figure's useful flops)")
+    res = _gpu_line("prefill_attention", t, flops=flops, cpu=cpu)
     res["seq"] = S
     return res
 
@@ -696,10 +731,14 @@ def cpu_baseline_int4(torch, inputs, budget_s):
     }
 
 
-def cpu_baseline_model(torch, budget_s, prompt_len=16):
-    """The oracle's fp32 Llama forward (restated llama_cpu.py) on the host cores:
-    Llama-3.2-1B shape, random fp32 weights, a short prompt, then greedy decode
-    steps until the time budget is spent (a bounded sample of config 5's decode)."""
+def cpu_baseline_model(torch, budget_s, prompt_len=512, long_ctx=3968):
+    """The oracle's fp32 Llama forward (restated llama_cpu.py) on the host cores,
+    Llama-3.2-1B shape, random fp32 weights, at config 5's windows beside the
+    GPU figures: the 512-token prefill (TTFT), greedy decode steps after it (KV
+    512 on), and greedy decode steps at KV 3968 on. The long window's cache is
+    filled with random K/V rows instead of a 3968-token CPU prefill: a decode
+    step's work does not depend on the cached values. Each decode window gets
+    half of budget_s (a bounded sample)."""
     from iron_amd.applications.llama_3_2_1b import LlamaConfig, random_weights
     from iron_amd.applications.llama_3_2_1b.model import compute_rope_angles
     from oracle import llama as ollama
@@ -710,25 +749,38 @@ def cpu_baseline_model(torch, budget_s, prompt_len=16):
     t0 = time.perf_counter()
     w = {k: v.float() for k, v in random_weights(cfg, torch.device("cpu"), seed=0).items()}
     shape = ollama.LlamaShape(cfg.vocab_size, cfg.emb_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_groups, cfg.hidden_dim)
-    ref = ollama.LlamaCPU(shape, w, compute_rope_angles(cfg.head_dim, 1024, cfg.rope_base, cfg.rope_scaling))
+    ref = ollama.LlamaCPU(shape, w, compute_rope_angles(cfg.head_dim, long_ctx + 512, cfg.rope_base, cfg.rope_scaling))
     setup_s = time.perf_counter() - t0
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab_size, (1, prompt_len), generator=g)
+
+    def decode(logits, kv0, budget):
+        steps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            logits = ref.forward(torch.tensor([[int(logits.argmax())]]), last_only=True)[0, -1]
+            steps += 1
+        dt = time.perf_counter() - t0
+        return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                "sample": f"{steps} greedy decode steps of the oracle's fp32 Llama forward (restated llama_cpu.py), "
+                f"Llama-3.2-1B shape, random weights, KV {kv0}..{kv0 + steps}, {dt:.1f} s"}
+
     ref.reset()
-    logits = ref.forward(prompt)[0, -1]
-    steps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and prompt_len + steps < 1024:
-        logits = ref.forward(torch.tensor([[int(logits.argmax())]]))[0, -1]
-        steps += 1
-    dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    logits = ref.forward(prompt, last_only=True)[0, -1]
+    ttft = time.perf_counter() - t0
+    short = decode(logits, prompt_len, budget_s / 2)
+    # the long window: caches of long_ctx random rows (bf16-representable, like the GPU's)
+    for i in range(shape.n_layers):
+        ref.kc[i] = torch.randn(1, shape.n_kv_groups, long_ctx, shape.head_dim, generator=g).bfloat16().float()
+        ref.vc[i] = torch.randn(1, shape.n_kv_groups, long_ctx, shape.head_dim, generator=g).bfloat16().float()
+    long = decode(logits, long_ctx, budget_s / 2)
     return {
-        "value": round(steps / dt, 3),
-        "unit": "tok/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{steps} greedy decode steps of the oracle's fp32 Llama forward (restated llama_cpu.py), "
-        f"Llama-3.2-1B shape, random weights, after a {prompt_len}-token prompt (KV {prompt_len}..{prompt_len + steps}); "
-        f"{dt:.1f} s (+{setup_s:.1f} s weight setup)",
+        "ttft_ms_512": {"value": round(ttft * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+                        "sample": f"one {prompt_len}-token prefill of the oracle's fp32 Llama forward (last position's "
+                        "logits), Llama-3.2-1B shape"},
+        "decode_kv512": short,
+        "decode_kv3968": long,
+        "setup_s": round(setup_s, 1),
     }
 
 
@@ -804,8 +856,16 @@ def main() -> int:
     i4 = bench_gemv_int4(torch, lib, tm, dev, args.steps, args.warmup)
     value = i4["bytes"] * args.steps / (i4["wall_ms"] * 1e-3) / 1e9
     kernel_us = i4["wall_ms"] * 1e3 / args.steps
-    achieved = i4["bytes"] / kernel_us / 1e3
+    achieved_live = i4["bytes"] / kernel_us / 1e3
     metric_lines("gemv_int4_cfg2", kernel_us, i4["bytes"])
+    # The roofline uses the kernel duration rocprofv3's kernel trace reports for
+    # this command's dispatches (each traced dispatch carries its own completion
+    # signal, so it is longer than the untraced per-step time above, which stays
+    # the headline value), so that the line and profiles/ agree.
+    trace_ns = profile_value(TRACE_PROFILE, "avg_ns")
+    traffic = profile_value(PMC_PROFILE, "traffic_bytes")
+    kernel_us_roof = trace_ns / 1e3 if trace_ns else kernel_us
+    achieved = i4["bytes"] / kernel_us_roof / 1e3
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -838,9 +898,16 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": TRAFFIC_BYTES,
+            "traffic": int(traffic) if traffic else None,
             "kernel": "gemv_i4_fast<1, 2, 1, false, 0>",
-            "kernel_us": round(kernel_us, 3),
+            "kernel_us": round(kernel_us_roof, 3),
+            "kernel_us_source": TRACE_PROFILE if trace_ns else "live (profile missing)",
+            "traffic_source": PMC_PROFILE if traffic else None,
+            "kernel_us_live": round(kernel_us, 3),
+            "achieved_live": round(achieved_live, 2),
+            "frac_live": round(achieved_live / HBM_PEAK_GBS, 4),
+            "live_timing": "untraced per-step device time of this run (the headline value); the kernel trace's "
+            "per-dispatch duration includes a completion signal per dispatch",
         },
     }
     if args.mode == "gemv":
@@ -855,16 +922,18 @@ def main() -> int:
         extra = {
             "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300, cpu_s=cs),
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300, cpu_s=cs),
-            "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608),
+            "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608, cpu_s=cs),
             "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200, cpu_s=cs),
             "prefill_gemm_cfg5": bench_prefill_gemm(torch, lib, tm, dev, 100, cpu_s=cs),
-            "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20),
+            "prefill_attention_cfg5": bench_prefill_attention(torch, lib, tm, dev, 20, cpu_s=cs),
             "llama_cfg5": bench_model(torch, dev),
         }
         out["extra"] = extra
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_int4(torch, i4["inputs"], args.cpu_seconds)
-            out["cpu_baseline"]["model_decode"] = cpu_baseline_model(torch, args.cpu_seconds)
+            model_cpu = cpu_baseline_model(torch, args.cpu_seconds)
+            extra["llama_cfg5"]["cpu_baseline"] = model_cpu
+            out["cpu_baseline"]["model_decode"] = model_cpu["decode_kv3968"]
     print(json.dumps(out), flush=True)
     return 0
 

@@ -119,7 +119,8 @@ __device__ __forceinline__ int xcd_block(int enable) {
 
 // The epoch word of the one-launch decode step (its exchange tags) moves on
 // once per step; the head GEMV that ends the step does it, after every
-// workgroup of the step's launch has read the old value.
+// workgroup of the step's launch has read the old value. Only launches with
+// argmax keys pass an epoch: every thread of workgroup 0 reaches the end.
 __device__ __forceinline__ void advance_epoch(unsigned* epoch) {
   if (epoch && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     const unsigned e = *epoch + 1u;
@@ -131,7 +132,6 @@ __device__ __forceinline__ void advance_epoch(unsigned* epoch) {
 // flight. One wave per output row.
 template <int U, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
-  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int tile = xcd_block(a.xcd);
   const int row = tile * 4 + (threadIdx.x >> 6);
@@ -187,12 +187,12 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
   if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + tile, key);
+  advance_epoch(a.epoch);  // last: at the start it would serialise the argument loads
 }
 
 // Generic path: any K % 8 == 0; chunks streamed 4 per lane per iteration.
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mode) {
-  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int tile = xcd_block(a.xcd);
   const int row = tile * 4 + (threadIdx.x >> 6);
@@ -242,6 +242,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mo
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
   if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + tile, key);
+  advance_epoch(a.epoch);  // last: at the start it would serialise the argument loads
 }
 
 template <int U, bool PAIR>
@@ -304,7 +305,6 @@ struct I4Args {
 // wave share the x preparation.
 template <int GPL, int R, int KS, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
-  advance_epoch(a.epoch);
   static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int tile = xcd_block(a.xcd);
@@ -452,12 +452,12 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
     }
   }
   if (KS == 1 && a.keys) publish_key<R>(a.keys, tile, key, (static_cast<size_t>(a.M) + 3) / 4);
+  advance_epoch(a.epoch);  // last: at the start it would serialise the argument loads
 }
 
 // Generic path: any K % 32 == 0, one row per wave, groups streamed one at a time.
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) {
-  advance_epoch(a.epoch);
   const int lane = threadIdx.x & (kWave - 1);
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool active = row < a.M;
@@ -504,6 +504,7 @@ __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) 
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
   if (a.keys) publish_key(a.keys, blockIdx.x, key);
+  advance_epoch(a.epoch);
 }
 
 template <int GPL, int R, int KS, bool PAIR>
