@@ -341,10 +341,12 @@ def bench_gqa(torch, lib, tm, dev, n, L=2048, max_len=None, cpu_s=0.0):
     ws = torch.zeros(int(lib.iron_gqa_decode_workspace_bytes(H, Hkv, D, max_len)), dtype=torch.uint8, device=dev)
     stream = _lib.stream_handle(dev)
 
+    # the model's call: counters kept at zero by the caller (IRON_GQA_COUNTERS_ZERO), so the timed launch is
+    # the attention kernel alone; streaming K/V loads (caches cold, rotated)
     def launch(i, s):
-        _check(lib, lib.iron_gqa_decode(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), KC[i % copies].data_ptr(),
-                                        VC[i % copies].data_ptr(), ad.data_ptr(), angles.shape[0], out.data_ptr(),
-                                        ws.data_ptr(), H, Hkv, D, max_len, pos, None, 1.0 / math.sqrt(D), s))
+        _check(lib, lib.iron_gqa_decode_ex(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), KC[i % copies].data_ptr(),
+                                           VC[i % copies].data_ptr(), ad.data_ptr(), angles.shape[0], out.data_ptr(),
+                                           ws.data_ptr(), H, Hkv, D, max_len, pos, None, 1.0 / math.sqrt(D), 2, s))
 
     for i in range(20):
         launch(i, stream)

@@ -185,16 +185,20 @@ int iron_rope(const void* x, const void* angles, int angles_fp32, void* out, int
 
 /* Bytes of workspace iron_gqa_decode needs for this shape (-1 if invalid):
  * one arrival counter per KV head (a 128-byte line each), then the per-chunk
- * partial results. Zero-fill it once before the first call: the counters must
- * start at zero, and every call leaves them at zero. Calls that share one
- * workspace must be stream-ordered, and nothing else may write to it between
- * calls. */
+ * partial results. iron_gqa_decode needs no initialisation (it zeroes the
+ * counters itself before each call); iron_gqa_decode_ex with
+ * IRON_GQA_COUNTERS_ZERO skips that and relies on the caller instead: zero-fill
+ * the workspace once and let nothing but these calls write to it (every call
+ * leaves the counters at zero). Calls that share one workspace must be
+ * stream-ordered. */
 long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
 
 /* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}).
- * With n_kv_heads a multiple of 8 it is one kernel launch (each KV head's
- * chunks run on one XCD and the last of them to finish merges them there),
- * otherwise two (chunk partials, then a merge kernel):
+ * With n_kv_heads a multiple of 8, on a device whose workgroups with ids
+ * congruent mod 8 run on one XCD (iron_xcd_round_robin), it is one kernel
+ * launch after a one-wave counter reset (each KV head's chunks run on one XCD
+ * and the last of them to finish merges them there); otherwise the chunk
+ * partials, then a merge kernel:
  *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
  *                                               (angle_rows, 64) [cos,sin])
  *   k_cache[:, pos] = k', v_cache[:, pos] = v_new
@@ -213,10 +217,14 @@ int iron_gqa_decode(const void* q, const void* k_new, const void* v_new, void* k
  * between calls (a decode loop over all layers of a model whose caches fit the
  * 256 MB Infinity Cache), so the K/V reads are ordinary, allocating loads;
  * without it (iron_gqa_decode) they are streaming loads, which are faster when
- * the caches come from HBM on every call. Results are identical either way;
- * unknown flag bits are rejected (IRON_EINVAL) before anything runs. Same
- * reference interface as iron_gqa_decode (llama_npu.py:486-523). */
+ * the caches come from HBM on every call. IRON_GQA_COUNTERS_ZERO: the caller
+ * keeps the workspace's arrival counters at zero (see
+ * iron_gqa_decode_workspace_bytes), so the call skips resetting them (one
+ * kernel launch fewer). Results are identical either way; unknown flag bits
+ * are rejected (IRON_EINVAL) before anything runs. Same reference interface as
+ * iron_gqa_decode (llama_npu.py:486-523). */
 #define IRON_GQA_KV_RESIDENT 1
+#define IRON_GQA_COUNTERS_ZERO 2
 int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                        const float* angles, int angle_rows, void* out, void* workspace, int n_heads, int n_kv_heads,
                        int head_dim, int max_len, int pos, const int* pos_dev, float scale, int flags, void* stream);
@@ -229,11 +237,14 @@ int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void
  * serving loops, harnesses that forbid hipMalloc) can use it. Shapes whose
  * iron_gqa_decode_workspace_bytes() exceed the maximum are rejected
  * (IRON_EINVAL) before anything runs. Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (other streams, other threads) race;
- * stream-ordered calls are safe. Each call first zeroes the array's arrival
- * counters (a one-wave kernel; with n_kv_heads not a multiple of 8 there are
- * none), so nothing carries over from an earlier call, racing or not. Same
- * results as iron_gqa_decode.
+ * array: calls that overlap on one GPU (other streams, other threads) corrupt
+ * each other's counters and partials (a call's counter reset can land in the
+ * middle of another call); stream-ordered calls are safe, and each first
+ * zeroes the array's arrival counters (a one-wave kernel), so nothing carries
+ * over from an earlier call. The array's device address is looked up
+ * (hipGetSymbolAddress) by the first call on a device or by
+ * iron_gqa_decode_noalloc_max_bytes(): make one of them before capturing this
+ * call into a hipGraph. Same results as iron_gqa_decode.
  * No counterpart in the reference: it exists for the callers above. */
 long long iron_gqa_decode_noalloc_max_bytes(void);
 int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -397,6 +408,15 @@ int iron_qkv_rope_scatter_splitk(const float* partial, int splits, const float* 
                                  void* k_cache, void* v_cache, int seq, int n_heads, int n_kv_heads, int head_dim,
                                  int max_len, int pos0, void* stream);
 
+/* 1 when the current device dispatches workgroups whose linear ids agree
+ * mod 8 to one XCD (the one-launch merges of iron_gqa_decode and
+ * iron_llama_decode_fused rely on it), 0 when it does not or when it cannot
+ * be checked now: the first call per device launches a 64-workgroup probe on
+ * `stream` and reads its result back, which is not done while `stream` is
+ * being captured. The answer is cached per device. No reference counterpart
+ * (a property of this GPU that the attention merge needs). */
+int iron_xcd_round_robin(void* stream);
+
 /* ------------------------------------------ One-launch decode step ---- */
 
 /* Per-layer device pointers of the one-launch decode step (a device array of
@@ -442,7 +462,10 @@ long long iron_llama_decode_fused_exchange_bytes(int n_layers);
  * call) becomes nonzero (bits: 1 layer input, 2 position, 4 q/k/v, 8
  * attention output, 16 o_proj output, 32 h); a nonzero
  * *status also makes every later wait give up at once. flags:
- * IRON_GQA_KV_RESIDENT. Replaces the single fused decode dispatch of
+ * IRON_GQA_KV_RESIDENT. The launch is a persistent grid of 1024 workgroups
+ * that wait for each other: it is refused (IRON_EINVAL) unless the device
+ * holds all of them at once (4 per CU on 256 CUs) and iron_xcd_round_robin()
+ * holds. Replaces the single fused decode dispatch of
  * iron/applications/llama_3.2_1b/llama_npu.py:459-584 (its runlist minus
  * the LM head). */
 int iron_llama_decode_fused(const IronDecodeLayer* layers, int n_layers, const void* keys, int n_keys,

@@ -103,6 +103,48 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB
 
 
+def asan_runtime() -> Path | None:
+    """clang's AddressSanitizer runtime next to hipcc's clang (preloaded into
+    the Python process that loads the sanitized library), or None."""
+    root = Path(_hipcc()).resolve().parent.parent
+    for base in (root / "lib" / "llvm" / "lib" / "clang", Path("/opt/rocm/lib/llvm/lib/clang")):
+        hits = sorted(base.glob("*/lib/linux/libclang_rt.asan-x86_64.so")) if base.exists() else []
+        if hits:
+            return hits[-1]
+    return None
+
+
+def build_asan(out_dir: Path, jobs: int | None = None) -> Path:
+    """The library with its host code built under AddressSanitizer
+    (``libiron_hip_asan.so`` in out_dir): every entry point's argument checks
+    and error reporting are instrumented; the device code is the ordinary
+    gfx950 build (the sanitizer applies to the host side only). It is linked
+    without the sanitizer runtime, which the process that loads it preloads.
+    For CPU tests of the validation paths; the GPU library is build()'s."""
+    out_dir = Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    host_asan = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+    def one(src: Path) -> Path:
+        obj = out_dir / (src.stem + ".o")
+        cmd = [_hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), *host_asan, "-c", str(src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc (host asan) failed on {src.name}:\n{res.stderr[-2000:]}")
+        return obj
+
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(one, sources))
+    lib = out_dir / "libiron_hip_asan.so"
+    res = subprocess.run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(lib), *map(str, objs)],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"asan link failed:\n{res.stderr[-2000:]}")
+    return lib
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)

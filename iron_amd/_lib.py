@@ -73,6 +73,7 @@ QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
     "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
     "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
+    "iron_xcd_round_robin": (_I, [_P]),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
     "iron_probe_read_workgroups": (_LL, [_LL, _I]),

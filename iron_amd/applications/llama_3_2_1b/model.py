@@ -41,6 +41,7 @@ from ...common.graph import capture_graph
 
 BF16 = torch.bfloat16
 KV_RESIDENT = 1  # IRON_GQA_KV_RESIDENT of iron_gqa_decode_ex (include/iron_hip.h)
+COUNTERS_ZERO = 2  # IRON_GQA_COUNTERS_ZERO: the workspace's arrival counters are kept at zero
 
 
 @dataclass
@@ -308,7 +309,8 @@ class LlamaHIP:
         # table of per-layer pointers (IronDecodeLayer), the exchange area, the
         # epoch its tags carry and the status word its bounded waits report to.
         self.fused = bool(cfg.decode_fused and cfg.int4 and cfg.emb_dim == 2048 and cfg.hidden_dim == 8192
-                          and cfg.n_heads == 32 and cfg.n_kv_groups == 8 and cfg.max_seq_len % 64 == 0)
+                          and cfg.n_heads == 32 and cfg.n_kv_groups == 8 and cfg.max_seq_len % 64 == 0
+                          and cfg.max_seq_len <= 6144 and _lib.query("iron_xcd_round_robin", s) == 1)
         if self.fused:
             table = []
             for i, Ly in enumerate(self.layers):
@@ -392,7 +394,7 @@ class LlamaHIP:
             _lib.call("iron_gqa_decode_ex", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), self.angles.data_ptr(), self.angles.shape[0], self.attn.data_ptr(),
                       self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, 0,
-                      self.pos.data_ptr(), scale, self.kv_flags, s)
+                      self.pos.data_ptr(), scale, self.kv_flags | COUNTERS_ZERO, s)
             L["o"].gemv(self.attn, self.x, s, residual=self.x)
             L["gate"].gemv(self.x, self.h, s, norm_scale=True, eps=cfg.eps, pair=L["up"])
             L["down"].gemv(self.h, self.x, s, residual=self.x)

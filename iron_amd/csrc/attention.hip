@@ -410,15 +410,15 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
 
 // Checks and launches of one GQA decode step with its counters and partials
 // in `workspace` (iron_gqa_decode_workspace_bytes() of the shape, 256-byte
-// aligned); shared by the entry point that takes a workspace (counters kept
-// at zero between calls) and the one that uses the library's own scratch
-// array (clear_counters: zeroed before each call by a small kernel).
-// One launch (n_kv_heads a multiple of 8: each KV head's chunks on one XCD,
-// merged by the last to finish) or the partials kernel plus the merge kernel.
+// aligned). The arrival counters are zeroed by a small kernel first unless
+// the caller keeps them at zero (IRON_GQA_COUNTERS_ZERO).
+// One launch (n_kv_heads a multiple of 8 and the device dispatching workgroup
+// ids congruent mod 8 to one XCD: each KV head's chunks on one XCD, merged by
+// the last to finish) or the partials kernel plus the merge kernel.
 template <int G, bool RES>
-static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, hipStream_t s) {
+static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_launch, hipStream_t s) {
   const dim3 block(kDecThreads);
-  if (n_kv_heads % kXcds == 0) {
+  if (one_launch) {
     IRON_LAUNCH((gqa_decode_kernel<G, true, RES>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
   } else {
     IRON_LAUNCH((gqa_decode_kernel<G, false, RES>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
@@ -429,8 +429,9 @@ static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, hipStream_t
 static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
                              void* v_cache, const float* angles, int angle_rows, void* out, void* workspace,
                              int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev,
-                             float scale, void* stream, bool clear_counters, int flags) {
-  IRON_REQUIRE((flags & ~IRON_GQA_KV_RESIDENT) == 0, "%s: unknown flags 0x%x", who, static_cast<unsigned>(flags));
+                             float scale, void* stream, int flags) {
+  IRON_REQUIRE((flags & ~(IRON_GQA_KV_RESIDENT | IRON_GQA_COUNTERS_ZERO)) == 0, "%s: unknown flags 0x%x", who,
+               static_cast<unsigned>(flags));
   IRON_REQUIRE(q && k_new && v_new && k_cache && v_cache && angles && out && workspace, "%s: null pointer", who);
   IRON_REQUIRE(head_dim == kD, "%s: head_dim=%d (only 64 is supported)", who, head_dim);
   IRON_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0,
@@ -462,21 +463,22 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.nsplit = decode_nsplit(max_len);
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (n_kv_heads % kXcds == 0 && clear_counters)
+  const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(s) == 1;
+  if (one && !(flags & IRON_GQA_COUNTERS_ZERO))
     IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
   if (flags & IRON_GQA_KV_RESIDENT) {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, s); break;
-      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, s); break;
-      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, s); break;
-      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, s); break;
+      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, one, s); break;
+      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, one, s); break;
+      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, one, s); break;
+      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, one, s); break;
     }
   } else {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, s); break;
-      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, s); break;
-      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, s); break;
-      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, s); break;
+      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, one, s); break;
+      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, one, s); break;
+      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, one, s); break;
+      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, one, s); break;
     }
   }
   return check_launch(who);
@@ -487,7 +489,7 @@ extern "C" int iron_gqa_decode(const void* q, const void* k_new, const void* v_n
                                int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
                                void* stream) {
   return gqa_decode_launch("iron_gqa_decode", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, workspace,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false, 0);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, 0);
 }
 
 extern "C" int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -495,8 +497,7 @@ extern "C" int iron_gqa_decode_ex(const void* q, const void* k_new, const void* 
                                   int n_kv_heads, int head_dim, int max_len, int pos, const int* pos_dev, float scale,
                                   int flags, void* stream) {
   return gqa_decode_launch("iron_gqa_decode_ex", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out,
-                           workspace, n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, false,
-                           flags);
+                           workspace, n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, flags);
 }
 
 // The workspace of iron_gqa_decode_noalloc: a file-scope device array, one
@@ -538,7 +539,13 @@ static void* decode_scratch_ptr(const char* who) {
   return g_scratch_ptr[dev];
 }
 
-extern "C" long long iron_gqa_decode_noalloc_max_bytes(void) { return kDecodeScratchBytes; }
+// Also resolves the calling device's scratch address (a hipGetSymbolAddress,
+// which is not to be called under graph capture): call it once outside
+// capture, and a captured iron_gqa_decode_noalloc only reads the cached address.
+extern "C" long long iron_gqa_decode_noalloc_max_bytes(void) {
+  decode_scratch_ptr("iron_gqa_decode_noalloc_max_bytes");
+  return kDecodeScratchBytes;
+}
 
 extern "C" int iron_gqa_decode_noalloc(const void* q, const void* k_new, const void* v_new, void* k_cache,
                                        void* v_cache, const float* angles, int angle_rows, void* out, int n_heads,
@@ -553,7 +560,7 @@ extern "C" int iron_gqa_decode_noalloc(const void* q, const void* k_new, const v
   void* ws = decode_scratch_ptr("iron_gqa_decode_noalloc");
   if (!ws) return IRON_EINVAL;
   return gqa_decode_launch("iron_gqa_decode_noalloc", q, k_new, v_new, k_cache, v_cache, angles, angle_rows, out, ws,
-                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, true, 0);
+                           n_heads, n_kv_heads, head_dim, max_len, pos, pos_dev, scale, stream, 0);
 }
 
 extern "C" int iron_attention_prefill(const void* q, const void* k, const void* v, void* out, int n_heads,

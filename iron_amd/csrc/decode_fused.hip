@@ -748,8 +748,12 @@ extern "C" int iron_llama_decode_fused(const IronDecodeLayer* layers, int n_laye
   a.wait_ticks = wait_us * 100u;
   IRON_REQUIRE(kNKV * a.nsplit <= kWgA, "%s: max_len=%d exceeds %d (one attention chunk per workgroup)", who, max_len,
                kWgA / kNKV * kDecChunk);
-  // every workgroup waits for others: the whole grid must be resident at once
+  // every workgroup waits for others: the whole grid must be resident at once;
+  // the attention merge needs each KV head's chunks on one XCD
   if (int rc = check_residency(who, (flags & IRON_GQA_KV_RESIDENT) != 0)) return rc;
+  IRON_REQUIRE(xcd_round_robin(static_cast<hipStream_t>(stream)) == 1,
+               "%s: workgroup ids congruent mod 8 do not share an XCD here, or that could not be checked (the first "
+               "check per device cannot run under stream capture)", who);
   const dim3 g(kGrid), blk(256);
   if (flags & IRON_GQA_KV_RESIDENT)
     IRON_LAUNCH(decode_step_kernel<true>, g, blk, 0, static_cast<hipStream_t>(stream), a);

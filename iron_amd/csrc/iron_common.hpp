@@ -208,6 +208,10 @@ struct TimingEvents {
 };
 TimingEvents take_timing_events();  // events for this launch (start only on the first)
 void disarm_timing();               // end of an entry point (called by check_launch)
+// 1 when workgroups whose linear ids agree mod 8 run on one XCD of the current
+// device (checked once per device, then cached); 0 when they do not, or when
+// it cannot be checked now (`stream` is being captured).
+int xcd_round_robin(hipStream_t stream);
 }  // namespace iron
 
 // Every kernel launch goes through here: with timing events armed, the launch

@@ -9,6 +9,8 @@
 #include "iron_common.hpp"
 #include "../../include/iron_hip.h"
 
+#include <mutex>
+
 namespace iron {
 namespace {
 
@@ -176,3 +178,48 @@ extern "C" int iron_probe_xcc_ids(int workgroups, void* ids, void* stream) {
               static_cast<int*>(ids));
   return check_launch("probe_xcc_ids");
 }
+
+// ---------------------------------------------------------------------------
+// The XCD dispatch mapping the one-launch attention merge relies on: workgroup
+// ids that agree mod 8 run on one XCD. Checked once per device with the probe
+// kernel above (64 workgroups; the ids land in a file-scope device array, so
+// nothing is allocated) and cached; not checked while `stream` is being
+// captured (the check reads its result back on the host), in which case the
+// answer is 0 for now and the callers take their paths that do not need it.
+// ---------------------------------------------------------------------------
+static constexpr int kXccProbeWgs = 64;
+static __device__ int g_xcc_ids[kXccProbeWgs];
+
+int iron::xcd_round_robin(hipStream_t stream) {
+  static std::mutex m;
+  static int state[64];  // per device: 0 unknown, 1 holds, -1 does not
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(m);
+  if (state[dev]) return state[dev] > 0 ? 1 : 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return 0;
+  int nx = 0;
+  if (hipDeviceGetAttribute(&nx, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || nx != 8) {
+    state[dev] = -1;
+    return 0;
+  }
+  void* ids_dev = nullptr;
+  if (hipGetSymbolAddress(&ids_dev, HIP_SYMBOL(g_xcc_ids)) != hipSuccess || !ids_dev) return 0;
+  hipLaunchKernelGGL(xcc_id_kernel, dim3(kXccProbeWgs), dim3(kProbeThreads), 0, stream, static_cast<int*>(ids_dev));
+  int ids[kXccProbeWgs];
+  if (hipGetLastError() != hipSuccess ||
+      hipMemcpyAsync(ids, ids_dev, sizeof(ids), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return 0;
+  bool ok = true, seen[16] = {};
+  for (int b = 0; b < kXccProbeWgs; ++b) ok &= ids[b] == ids[b % 8];
+  for (int b = 0; b < 8 && ok; ++b) {
+    ok &= ids[b] >= 0 && ids[b] < 16 && !seen[ids[b]];
+    if (ok) seen[ids[b]] = true;
+  }
+  state[dev] = ok ? 1 : -1;
+  return ok ? 1 : 0;
+}
+
+extern "C" int iron_xcd_round_robin(void* stream) { return xcd_round_robin(static_cast<hipStream_t>(stream)); }

@@ -126,8 +126,8 @@ def test_offset_limits_rejected_on_host():
 
 
 def test_gqa_decode_ex_rejects_unknown_flags_on_host():
-    """Flag bits other than IRON_GQA_KV_RESIDENT are refused before anything runs."""
+    """Flag bits other than IRON_GQA_KV_RESIDENT and IRON_GQA_COUNTERS_ZERO are refused before anything runs."""
     from iron_amd import _lib
 
     with pytest.raises(_lib.IronHipError, match="unknown flags"):
-        _lib.call("iron_gqa_decode_ex", 16, 16, 16, 16, 16, 16, 128, 16, 256, 32, 8, 64, 128, 0, None, 0.125, 2, None)
+        _lib.call("iron_gqa_decode_ex", 16, 16, 16, 16, 16, 16, 128, 16, 256, 32, 8, 64, 128, 0, None, 0.125, 4, None)

@@ -32,10 +32,11 @@ def test_app_check_accuracy(gpu):
     prefill_kl = float(re.search(r"\[Accuracy\] Prefill KL:\s*(\S+)", res.stdout).group(1))
     decode_kl = float(re.search(r"\[Accuracy\] Decode max KL:\s*(\S+)", res.stdout).group(1))
     mism = int(re.search(r"\[Accuracy\] Top-1 mismatches:\s*(\d+)", res.stdout).group(1))
-    # the reference gates the KL values only (test.py:93-95); mismatches are a reported metric
+    # the reference gates the KL values only (test.py:93-95); here top-1 is gated too, allowing the bf16
+    # near-ties of random-init logits (nearly flat: test_llama_cfg5_gpu.py saw 5 in 128 steps)
     assert prefill_kl <= MAX_PREFILL_KL, prefill_kl
     assert decode_kl <= MAX_DECODE_KL, decode_kl
-    assert 0 <= mism <= 17, mism
+    assert 0 <= mism <= 2, mism
 
 
 def test_app_check_determinism(gpu):

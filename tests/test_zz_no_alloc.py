@@ -68,3 +68,36 @@ def test_noalloc_group_sizes(gpu):
         got = _run(gpu, c, noalloc=True)
         for w, g in zip(want, got):
             assert torch.equal(w.view(torch.int16), g.view(torch.int16))
+
+
+def test_noalloc_captured_in_a_graph(gpu):
+    """iron_gqa_decode_noalloc captured into a hipGraph (its scratch address
+    looked up beforehand, outside capture, by the max-bytes query) and replayed
+    several times, with the program's own eager work between the replays:
+    every replay's output and cache append equal iron_gqa_decode's bit for bit
+    (the replay re-appends the same k/v row, so each replay computes the same)."""
+    from iron_amd import _lib
+    from iron_amd.common.graph import capture_graph
+
+    assert _lib.query("iron_gqa_decode_noalloc_max_bytes") == 4 << 20
+    c = _case(gpu, L=1000, max_len=1024, seed=4)
+    print("noalloc under capture: kv 1000, max_len 1024", flush=True)
+    want = _run(gpu, c, noalloc=False)
+    kc, vc = c["kc"].clone(), c["vc"].clone()
+    out = torch.full((c["H"], 64), -1.0, dtype=torch.bfloat16, device=gpu)
+
+    def call():
+        _lib.call("iron_gqa_decode_noalloc", c["q"].data_ptr(), c["kn"].data_ptr(), c["vn"].data_ptr(),
+                  kc.data_ptr(), vc.data_ptr(), c["angles"].data_ptr(), c["angles"].shape[0], out.data_ptr(),
+                  c["H"], c["Hkv"], 64, c["max_len"], c["pos"], None, 0.125, _lib.stream_handle(gpu))
+
+    call()  # eager first: code object loaded
+    torch.cuda.synchronize()
+    graph = capture_graph(call, gpu)
+    for r in range(4):
+        out.fill_(-1.0)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want[0].view(torch.int16)), f"replay {r}"
+        assert torch.equal(kc.view(torch.int16), want[1].view(torch.int16)), f"replay {r}"
+        assert torch.equal(vc.view(torch.int16), want[2].view(torch.int16)), f"replay {r}"
