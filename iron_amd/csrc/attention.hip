@@ -7,6 +7,7 @@
 #include "decode_attn.hpp"
 #include "../../include/iron_hip.h"
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -415,13 +416,34 @@ extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads
 // One launch (n_kv_heads a multiple of 8 and the device dispatching workgroup
 // ids congruent mod 8 to one XCD: each KV head's chunks on one XCD, merged by
 // the last to finish) or the partials kernel plus the merge kernel.
+// CUs of the current device (cached per device; 256 if it cannot be read).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c;
+}
+
 template <int G, bool RES>
 static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_launch, hipStream_t s) {
   const dim3 block(kDecThreads);
   if (one_launch) {
-    IRON_LAUNCH((gqa_decode_kernel<G, true, RES>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
+    // 128-position chunks (kDecWaves1 waves) when the cache is long enough for
+    // one per CU, else 64; the workspace holds the 64-position partials either way
+    DecodeArgs b = a;
+    b.nsplit = (a.max_len + 16 * kDecWaves1 - 1) / (16 * kDecWaves1);
+    if (b.nsplit * n_kv_heads >= device_cus())
+      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1>), dim3(b.nsplit * n_kv_heads), dim3(kDecWaves1 * kWave),
+                  0, s, b);
+    else
+      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, 4>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
   } else {
-    IRON_LAUNCH((gqa_decode_kernel<G, false, RES>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
+    IRON_LAUNCH((gqa_decode_kernel<G, false, RES, 4>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
     IRON_LAUNCH((gqa_combine_kernel<G>), dim3(n_kv_heads * G), dim3(kMergeThreads), 0, s, a);
   }
 }
@@ -445,6 +467,8 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
                    aligned16(angles),
                "%s: q, k_new, v_new, the caches and the angle table must be 16-byte aligned", who);
   IRON_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255u) == 0, "%s: workspace must be 256-byte aligned", who);
+  IRON_REQUIRE(decode_head_stride(G, max_len) * 4 < (1LL << 31),
+               "%s: max_len=%d: a KV head's chunk partials exceed the 2 GiB the merge addresses", who, max_len);
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k_new = static_cast<const uint16_t*>(k_new);

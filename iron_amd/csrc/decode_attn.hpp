@@ -11,7 +11,8 @@
 // When Hkv is a multiple of 8 the merge happens in the same launch: all
 // chunks of one KV head run on one XCD (workgroups are dispatched to the 8
 // XCDs round-robin), so their partials meet in that XCD's L2, and the last
-// workgroup of the head to count itself in (an atomic in that L2) merges them.
+// workgroup of the head to count itself in (an atomic in that L2) merges them,
+// one wave per query head.
 // A merge across XCDs in one launch was measured slower than a second launch:
 // it needs an agent-scope release (a write-back of the whole per-XCD L2,
 // serialised across workgroups) or write-through stores and device-scope
@@ -37,8 +38,9 @@
 namespace iron {
 namespace {
 
-constexpr int kDecChunk = 64;  // cache positions per workgroup (4 waves x 16)
+constexpr int kDecChunk = 64;  // cache positions per workgroup of 4 waves (16 per wave)
 constexpr int kDecThreads = 256;
+constexpr int kDecWaves1 = 8;  // waves per workgroup of the one-launch path on long caches (128 positions)
 constexpr int kD = 64;         // head dim (the reference MHA supports d = 64 only)
 
 struct DecodeArgs {
@@ -60,8 +62,8 @@ struct DecodeArgs {
   float scale_log2;       // log2(e) * scale
 };
 
-// One chunk's partial: G x 64 unnormalised outputs, then G maxima, then G
-// sums, padded to a whole number of 16-byte quads.
+// One chunk's partial: G x 64 unnormalised outputs, then (maximum, sum) of
+// each of the G heads as one 8-byte pair, padded to a whole number of 16-byte quads.
 template <int G>
 constexpr int part_stride() {
   return (G * kD + 2 * G + 3) / 4 * 4;
@@ -94,7 +96,7 @@ __device__ __forceinline__ void rope_chunk(const uint4 own, const uint4 pair, co
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float c = ang[2 * e], s = ang[2 * e + 1];
-    const float r = lower ? xo[e] * c - xp[e] * s : xo[e] * c + xp[e] * s;
+    const float r = lower ? rot_sub(xo[e], c, xp[e], s) : rot_add(xo[e], c, xp[e], s);
     out[e] = bf16_to_f32(f32_to_bf16(r));
   }
 }
@@ -139,6 +141,7 @@ __device__ __forceinline__ float sum_over_rows(float a) {
 __device__ __forceinline__ float exp2_weight(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef __bf16 dec_bf16x8 __attribute__((ext_vector_type(8)));
+
 typedef short dec_i16x4 __attribute__((ext_vector_type(4)));
 typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
 
@@ -147,8 +150,12 @@ typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
 // land on disjoint bank groups. An involution in c.
 __device__ __forceinline__ int dec_v_slot(int R, int c) { return c ^ (((R >> 1) & 3) << 1); }
 
-// One decode step of KV head j for its G query heads; workgroup s owns cache
-// positions [64 s, 64 s + 64), wave w of it positions 64 s + 16 w + [0, 16).
+// One decode step of KV head j for its G query heads; a workgroup of NW waves
+// owns cache positions [CH s, CH s + CH), CH = 16 NW, wave w of it positions
+// CH s + 16 w + [0, 16). NW = 4 (64 positions), or 8 (128 positions) for
+// the one-launch path when that still gives at least one workgroup per CU:
+// half the partials for the merge to read and half the workgroups to
+// dispatch, for a longer wait on each CU's loads.
 //
 // Per wave, on the matrix cores (v_mfma_f32_16x16x32_bf16 for the scores,
 // v_mfma_f32_16x16x16_bf16 for the output):
@@ -173,13 +180,12 @@ __device__ __forceinline__ int dec_v_slot(int R, int c) { return c ^ (((R >> 1) 
 // and chunk t % nsplit, t = n / 8, so all chunks of a head run on one XCD.
 // After writing its partial a workgroup waits for its stores to reach that
 // XCD's L2 and counts itself in with an atomic there; the last of the head's
-// active chunks to arrive invalidates its CU's L1 and merges the head's
-// partials from the L2 (fused_merge), then returns the counter to zero. No
-// workgroup waits for another. Without MERGE the grid is (nsplit, Hkv) and
-// gqa_combine_kernel merges.
-// The cache rows one thread of chunk s of KV head j needs (they do not
-// depend on the position: rows past it are masked or replaced later). K: lane
-// l of wave w holds row 64 s + 16 w + l % 16, dims 8 (l / 16) + [0, 8) (k0)
+// active chunks to arrive returns the counter to zero and merges the head's
+// partials from the L2 (gqa_merge_heads). No workgroup waits for another.
+// Without MERGE the grid is (nsplit, Hkv) and gqa_combine_kernel merges.
+// The cache rows one thread of the chunk at positions p0 + [0, 16 NW) of KV
+// head j needs (they do not depend on the position: rows past it are masked
+// or replaced later). K: lane l of wave w holds row p0 + 16 w + l % 16, dims 8 (l / 16) + [0, 8) (k0)
 // and 32 + the same (k1). V: lane l of load u holds row 16 w + 8 u + l / 8,
 // 16-byte chunk dec_v_slot(row, l % 8), which the body stores into slot l % 8
 // of the wave's LDS block. Rows are clamped to the cache. RES: the caches stay
@@ -192,10 +198,10 @@ struct DecodeKv {
 };
 template <bool RES>
 __device__ __forceinline__ DecodeKv load_kv_rows(int tid, const uint16_t* k_cache, const uint16_t* v_cache,
-                                                 int max_len, int s, int j) {
+                                                 int max_len, int p0, int j) {
   const int lane = tid & (kWave - 1), w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, cq = lane >> 4;
-  const int wrow0 = s * kDecChunk + 16 * w;
+  const int wrow0 = p0 + 16 * w;
   const size_t hb = static_cast<size_t>(j) * max_len;
   auto ld_kv = [](const uint16_t* p) { return RES ? *reinterpret_cast<const uint4*>(p) : ld_stream16(p); };
   const int krow = min(wrow0 + r, max_len - 1);
@@ -214,7 +220,8 @@ __device__ __forceinline__ DecodeKv load_kv_rows(int tid, const uint16_t* k_cach
 template <int G>
 struct PlainDecodeIo {
   static constexpr bool kEarly = true;
-  static constexpr int kMergeLoads = 16;
+  static constexpr bool kStaleL1 = false;  // a kernel starts with its L1 invalidated
+  static constexpr int kMergeChunks = 16;   // merge loads in flight per lane
   const DecodeArgs& a;
   __device__ __forceinline__ void new_kv(int j, int cq, uint4& kna, uint4& knb, uint4& vna, uint4& vnb) const {
     kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * kD + cq * 8);
@@ -230,21 +237,22 @@ struct PlainDecodeIo {
   __device__ __forceinline__ bool wait_inputs(int) const { return true; }
   __device__ __forceinline__ int thread() const { return threadIdx.x; }
   template <bool RES>
-  __device__ __forceinline__ DecodeKv kv_rows(const DecodeArgs& d, int s, int j) const {
-    return load_kv_rows<RES>(threadIdx.x, d.k_cache, d.v_cache, d.max_len, s, j);
+  __device__ __forceinline__ DecodeKv kv_rows(const DecodeArgs& d, int p0, int j) const {
+    return load_kv_rows<RES>(threadIdx.x, d.k_cache, d.v_cache, d.max_len, p0, j);
   }
   __device__ __forceinline__ void store_out(size_t off, uint32_t lo, uint32_t hi) const {
     *reinterpret_cast<uint2*>(a.out + off) = make_uint2(lo, hi);
   }
 };
 
-template <int G, class Io>
-__device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid, const Io& io);
+template <int G, int NW, class Io>
+__device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, const Io& io);
 
-template <int G, bool MERGE, bool RES, class Io>
+template <int G, bool MERGE, bool RES, int NW, class Io>
 __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int j, int pos, Io& io) {
   constexpr int D = kD;
-  constexpr int NW = kDecThreads / kWave;
+  constexpr int NT = NW * kWave;   // threads
+  constexpr int CH = NW * 16;      // cache positions
   constexpr int PS = part_stride<G>();
   __shared__ __attribute__((aligned(16))) uint16_t q_s[G * D];  // rotated q, bf16
   __shared__ float wm_s[NW][G], wl_s[NW][G];
@@ -254,7 +262,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   const int tid = io.thread(), lane = tid & (kWave - 1), w = tid >> 6;
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
-  const int p0 = s * kDecChunk;
+  const int p0 = s * CH;
   if (p0 >= L) return;
   const int r = lane & 15, cq = lane >> 4;
   const int wrow0 = p0 + 16 * w;
@@ -283,12 +291,12 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     }
     if constexpr (Io::kEarly) io.new_kv(j, cq, kna, knb, vna, vnb);
   }
-  constexpr int QN = (G * D + kDecThreads - 1) / kDecThreads;  // q elements per thread
+  constexpr int QN = (G * D + NT - 1) / NT;  // q elements per thread
   uint16_t qx[QN], qp[QN];
   float2 qa[QN];
 #pragma unroll
   for (int e = 0; e < QN; ++e) {
-    const int t = min(tid + kDecThreads * e, G * D - 1), i = (t % D) & 31;
+    const int t = min(tid + NT * e, G * D - 1), i = (t % D) & 31;
     if constexpr (Io::kEarly) io.q_pair(j, t, qx[e], qp[e]);
     qa[e] = *reinterpret_cast<const float2*>(angrow + 2 * i);
   }
@@ -298,7 +306,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // positions fits the Infinity Cache while the weights stream past it), so the
   // K/V loads are ordinary, allocating loads (decode +0.9%). Otherwise they are
   // streaming loads, faster when the caches come from HBM every time.
-  const DecodeKv kv = io.template kv_rows<RES>(a, s, j);
+  const DecodeKv kv = io.template kv_rows<RES>(a, p0, j);
   uint4 k0 = kv.k0, k1 = kv.k1;
   unsigned char* vblk = v_s[w];
   const uint4 vraw[2] = {kv.v0, kv.v1};
@@ -306,14 +314,14 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     if (!io.wait_inputs(j)) return;  // workgroup-uniform
     if (owner) io.new_kv(j, cq, kna, knb, vna, vnb);
 #pragma unroll
-    for (int e = 0; e < QN; ++e) io.q_pair(j, min(tid + kDecThreads * e, G * D - 1), qx[e], qp[e]);
+    for (int e = 0; e < QN; ++e) io.q_pair(j, min(tid + NT * e, G * D - 1), qx[e], qp[e]);
   }
 #pragma unroll
   for (int e = 0; e < QN; ++e) {
-    const int t = tid + kDecThreads * e;
+    const int t = tid + NT * e;
     if (t < G * D) {
       const float x = bf16_to_f32(qx[e]), xp = bf16_to_f32(qp[e]);
-      q_s[t] = f32_to_bf16((t % D) < 32 ? x * qa[e].x - xp * qa[e].y : x * qa[e].x + xp * qa[e].y);
+      q_s[t] = f32_to_bf16((t % D) < 32 ? rot_sub(x, qa[e].x, xp, qa[e].y) : rot_add(x, qa[e].x, xp, qa[e].y));
     }
   }
   // barrier without a wait for the K/V loads in flight (__syncthreads would
@@ -425,7 +433,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
 
   // the chunk's partial: the four waves merged
   float* part = a.part + static_cast<size_t>(j) * a.head_stride + static_cast<size_t>(s) * PS;
-  for (int t = tid; t < G * D; t += kDecThreads) {
+  for (int t = tid; t < G * D; t += NT) {
     const int g = t / D;
     float M = wm_s[0][g];  // finite: position p0 < L is in wave 0
 #pragma unroll
@@ -438,17 +446,14 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
       l = fmaf(f, wl_s[ww][g], l);
     }
     part[t] = o;
-    if (t % D == 0) {
-      part[G * D + g] = M;
-      part[G * D + G + g] = l;
-    }
+    if (t % D == 0) *reinterpret_cast<float2*>(part + G * D + 2 * g) = make_float2(M, l);
   }
   if constexpr (MERGE) {
     __shared__ int last_s;
-    const int nact = (L + kDecChunk - 1) / kDecChunk;
+    const int nact = (L + CH - 1) / CH;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have reached the L2
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0) {  // an atomic in the XCD's L2, where the partials are
       unsigned* c = a.ctr + static_cast<size_t>(j) * kCtrStride;
       const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       const int last = old == static_cast<unsigned>(nact - 1);
@@ -457,152 +462,104 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     }
     __syncthreads();
     if (!last_s) return;
-    asm volatile("buffer_inv sc0" ::: "memory");  // no stale line of the head's partials in this CU's L1
-    fused_merge<G>(a, j, nact, tid, io);
+    if constexpr (Io::kStaleL1) asm volatile("buffer_inv sc1" ::: "memory");
+    gqa_merge_heads<G, NW>(a, j, nact, tid, io);
   }
 }
 
-// The merge of KV head j's nact chunk partials by one 256-thread workgroup,
-// in batches of 64 chunks. Per batch, the statistics first: one wave per
-// head takes the batch's 64 maxima (a DPP reduction), raises the head's
-// running maximum, and leaves each chunk's weight exp2(M_c - M) in LDS, with
-// the running sum and the factor that rescales the earlier batches. Then the
-// outputs: thread -> 4 consecutive values (quad qd of the G x 64) and slice q
-// of the chunks (c0 + q + NQ b), its weights read as one vector from LDS, one
-// FMA per value and chunk. The loads of the statistics and of the outputs are
-// all issued before the statistics are used (one round trip); chunks past
-// nact load chunk nact - 1 and weigh 0, and the number of output loads per
-// thread is the live count rounded up to 4, 8 or 16. The NQ slices meet in LDS
-// at the end. Every sum runs in a fixed order: the result depends only on the
-// data.
-template <int G, class Io>
-__device__ void fused_merge(const DecodeArgs& a, int j, int nact, int tid, const Io& io) {
+// The merge of KV head j's nact chunk partials by the workgroup that finished
+// last, one wave per query head (heads w, w + NW, ...; waves >= G idle).
+// Lane -> output quad qd = lane % 16 (dims 4 qd .. 4 qd + 3) and chunk slice
+// r = lane / 16 (chunks r, r + 4, ...): per chunk one 16-byte load of the
+// outputs and one 8-byte load of (maximum, sum), a round of B chunks per lane
+// all in flight together (B = 8 or 16 by the active count, capped by
+// Io::kMergeChunks; more chunks take more rounds). Each slice folds its chunks
+// with a running maximum and the four slices meet by permlane swaps: no LDS
+// and no barrier. The partials were written to the XCD's L2 by other CUs; a
+// kernel starts with its L1 invalidated and no CU reads a head's partials
+// before its merge, so plain loads see them (an Io whose persistent
+// workgroups merge again later invalidates its L1 first, Io::kStaleL1).
+// Every sum runs in a fixed order: the result depends only on the data.
+template <int G, int NW, class Io>
+__device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, const Io& io) {
   constexpr int D = kD;
   constexpr int PS = part_stride<G>();
-  constexpr int CB = 64;                      // chunks per batch
-  constexpr int NQD = G * D / 4;              // output quads per chunk
-  constexpr int NQ = kDecThreads / NQD;       // chunk slices
-  constexpr int PER = CB / NQ;                // chunks per thread per batch
-  constexpr int NE = (CB * G + kDecThreads - 1) / kDecThreads;  // (head, chunk) pairs per thread
-  __shared__ __attribute__((aligned(16))) float w_s[G * CB];    // [head][slice][b]
-  __shared__ float mh_s[G], lh_s[G], sc_s[G];
-  __shared__ float4 oo_s[kDecThreads];
-  const int lane = tid & (kWave - 1);
-  const int qd = tid % NQD, q = tid / NQD, g = qd / (D / 4);
+  constexpr int NS = kWave / (D / 4);  // chunk slices per wave
+  const int lane = tid & (kWave - 1), w = tid >> 6, qd = lane & (D / 4 - 1), r = lane / (D / 4);
   const float* base = a.part + static_cast<size_t>(j) * a.head_stride;
-  if (tid < G) {
-    mh_s[tid] = -INFINITY;
-    lh_s[tid] = 0.f;
-  }
-  __syncthreads();
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto load_o = [&](int c0, int b) {
-    return *reinterpret_cast<const float4*>(base + static_cast<size_t>(min(c0 + q + NQ * b, nact - 1)) * PS + 4 * qd);
-  };
-  // one batch with N (<= 16) output loads per thread per round
-  auto batch = [&](auto n_tag, int c0, bool one_round) {
-    constexpr int N = decltype(n_tag)::value;
-    float st_m[NE], st_l[NE];
+  const int span = (nact + NS - 1) / NS;  // chunks of slice 0
+  for (int g = w; g < G; g += NW) {
+    float m = -INFINITY, l = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto round = [&](auto b_tag, int c0) {
+      constexpr int B = decltype(b_tag)::value;
+      float2 st[B];
+      float4 ob[B];
 #pragma unroll
-    for (int e = 0; e < NE; ++e) {
-      const int p = tid + kDecThreads * e, h = min(p / CB, G - 1), c = c0 + p % CB;
-      const float* pk = base + static_cast<size_t>(min(c, nact - 1)) * PS;
-      st_m[e] = pk[G * D + h];
-      st_l[e] = pk[G * D + G + h];
-    }
-    __builtin_amdgcn_sched_barrier(0);  // statistics first: their wait leaves the output loads in flight
-    float4 ob[N];
-#pragma unroll
-    for (int b = 0; b < N; ++b) ob[b] = load_o(c0, b);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int e = 0; e < NE; ++e) {
-      const int p = tid + kDecThreads * e;
-      if (p < CB * G) {  // whole waves: one head each
-        const int h = p / CB, cb = p % CB;
-        const bool live = c0 + cb < nact;
-        const float m = live ? st_m[e] : -INFINITY;
-        const float mb = wave_max(m);  // finite: chunk c0 is live
-        const float mo = mh_s[h];
-        const float mn = fmaxf(mo, mb);
-        const float wgt = exp2_weight(m - mn);  // 0 past nact
-        w_s[(h * NQ + cb % NQ) * PER + cb / NQ] = wgt;
-        const float ls = wave_sum(live ? wgt * st_l[e] : 0.f);
-        if (lane == 0) {
-          const float sc = exp2_weight(mo - mn);  // 0 on the first batch
-          sc_s[h] = sc;
-          mh_s[h] = mn;
-          lh_s[h] = fmaf(lh_s[h], sc, ls);
-        }
+      for (int b = 0; b < B; ++b) {  // chunk c0 + r + NS b (past nact: chunk nact - 1, dropped below)
+        const float* pk = base + static_cast<size_t>(min(c0 + r + NS * b, nact - 1)) * PS;
+        st[b] = *reinterpret_cast<const float2*>(pk + G * D + 2 * g);
+        ob[b] = *reinterpret_cast<const float4*>(pk + g * D + 4 * qd);
       }
-    }
-    __syncthreads();
-    const float sc = sc_s[g];
-    acc.x *= sc;
-    acc.y *= sc;
-    acc.z *= sc;
-    acc.w *= sc;
-    const float* wrow = &w_s[(g * NQ + q) * PER];
+      float bm = m;
 #pragma unroll
-    for (int b0 = 0; b0 < PER; b0 += N) {
-      if (b0 > 0) {
-        if (c0 + q + NQ * b0 >= nact) break;  // no live chunk left in this slice
+      for (int b = 0; b < B; ++b)
+        if (c0 + r + NS * b < nact) bm = fmaxf(bm, st[b].x);  // a live chunk's maximum is finite
+      if (bm == -INFINITY) return;                            // no live chunk in this slice
+      const float keep = exp2_weight(m - bm);                 // 0 while m is -inf
+      acc.x *= keep;
+      acc.y *= keep;
+      acc.z *= keep;
+      acc.w *= keep;
+      l *= keep;
 #pragma unroll
-        for (int b = 0; b < N; ++b) ob[b] = load_o(c0, b0 + b);
+      for (int b = 0; b < B; ++b) {
+        const float wgt = c0 + r + NS * b < nact ? exp2_weight(st[b].x - bm) : 0.f;
+        acc.x = fmaf(wgt, ob[b].x, acc.x);
+        acc.y = fmaf(wgt, ob[b].y, acc.y);
+        acc.z = fmaf(wgt, ob[b].z, acc.z);
+        acc.w = fmaf(wgt, ob[b].w, acc.w);
+        l = fmaf(wgt, st[b].y, l);
       }
-      float wv[N];
-#pragma unroll
-      for (int b = 0; b < N; b += 4) {
-        const float4 t = *reinterpret_cast<const float4*>(wrow + b0 + b);
-        wv[b] = t.x;
-        wv[b + 1] = t.y;
-        wv[b + 2] = t.z;
-        wv[b + 3] = t.w;
-      }
-#pragma unroll
-      for (int b = 0; b < N; ++b) {
-        acc.x = fmaf(wv[b], ob[b].x, acc.x);
-        acc.y = fmaf(wv[b], ob[b].y, acc.y);
-        acc.z = fmaf(wv[b], ob[b].z, acc.z);
-        acc.w = fmaf(wv[b], ob[b].w, acc.w);
-      }
-      if (N < PER && b0 + N >= PER) break;
-      if (one_round) break;  // the batch covered the slice's live chunks
-    }
-    __syncthreads();  // w_s and sc_s are rewritten by the next batch
-  };
-  for (int c0 = 0; c0 < nact; c0 += CB) {
-    const int span = (min(CB, nact - c0) + NQ - 1) / NQ;  // live chunks per slice (uniform)
-    // Io::kMergeLoads caps the output loads in flight per thread (registers);
-    // a capped batch takes as many rounds as the slice needs
-    constexpr int NMAX = PER < Io::kMergeLoads ? PER : Io::kMergeLoads;
-    if (span <= 4 && PER >= 4)
-      batch(std::integral_constant<int, (PER < 4 ? PER : 4)>{}, c0, true);
-    else if (span <= 8 && NMAX >= 8)
-      batch(std::integral_constant<int, 8>{}, c0, true);
+      m = bm;
+    };
+    constexpr int BMAX = Io::kMergeChunks;
+    if (span <= 4)
+      round(std::integral_constant<int, 4>{}, 0);
+    else if (span <= 8 || BMAX < 16)
+      for (int c0 = 0; c0 < nact; c0 += NS * 8) round(std::integral_constant<int, 8>{}, c0);
     else
-      batch(std::integral_constant<int, NMAX>{}, c0, NMAX < 16 && NMAX >= span);
-  }
-  oo_s[tid] = acc;
-  __syncthreads();
-  if (q == 0) {
-    float4 ot = acc;
-#pragma unroll
-    for (int qq = 1; qq < NQ; ++qq) {
-      const float4 o = oo_s[qq * NQD + qd];
-      ot.x += o.x;
-      ot.y += o.y;
-      ot.z += o.z;
-      ot.w += o.w;
+      for (int c0 = 0; c0 < nact; c0 += NS * BMAX) round(std::integral_constant<int, BMAX>{}, c0);
+    // the four slices: rows r and r ^ 2, then r and r ^ 1 (x: the lower row)
+    auto fold = [&](auto split) {
+      float mx, my;
+      split(m, mx, my);
+      const float mn = fmaxf(mx, my);  // finite: slice 0 holds chunk 0
+      const float fx = mx == -INFINITY ? 0.f : exp2_weight(mx - mn), fy = my == -INFINITY ? 0.f : exp2_weight(my - mn);
+      auto mix = [&](float& v) {
+        float x, y;
+        split(v, x, y);
+        v = fmaf(fx, x, fy * y);
+      };
+      mix(acc.x);
+      mix(acc.y);
+      mix(acc.z);
+      mix(acc.w);
+      mix(l);
+      m = mn;
+    };
+    fold([](float v, float& x, float& y) { split32(v, x, y); });
+    fold([](float v, float& x, float& y) { split16(v, x, y); });
+    if (r == 0) {
+      const float rl = __builtin_amdgcn_rcpf(l);
+      io.store_out(static_cast<size_t>(j * G + g) * D + 4 * qd, cvt_pk_bf16(acc.x * rl, acc.y * rl),
+                   cvt_pk_bf16(acc.z * rl, acc.w * rl));
     }
-    const float rl = __builtin_amdgcn_rcpf(lh_s[g]);
-    const uint32_t lo = cvt_pk_bf16(ot.x * rl, ot.y * rl), hi = cvt_pk_bf16(ot.z * rl, ot.w * rl);
-    io.store_out(static_cast<size_t>(j) * G * D + 4 * qd, lo, hi);
   }
 }
 
-template <int G, bool MERGE, bool RES>
-__global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
+template <int G, bool MERGE, bool RES, int NW>
+__global__ __launch_bounds__(NW * kWave) void gqa_decode_kernel(DecodeArgs a) {
   int s, j;
   if constexpr (MERGE) {
     const int n = blockIdx.x, t = n / kXcds;
@@ -613,7 +570,7 @@ __global__ __launch_bounds__(kDecThreads) void gqa_decode_kernel(DecodeArgs a) {
     j = blockIdx.y;
   }
   PlainDecodeIo<G> io{a};
-  gqa_decode_chunk<G, MERGE, RES>(a, s, j, a.pos_dev ? *a.pos_dev : a.pos, io);
+  gqa_decode_chunk<G, MERGE, RES, NW>(a, s, j, a.pos_dev ? *a.pos_dev : a.pos, io);
 }
 
 // Merge of the chunk partials, one 1024-thread workgroup per query head
@@ -643,8 +600,8 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 #pragma unroll
   for (int b = 0; b < B; ++b) {
     const float* pk = base + static_cast<size_t>(min(q + b * NQ, a.nsplit - 1)) * PS;
-    mb[b] = pk[G * D + g];
-    lb[b] = pk[G * D + G + g];
+    mb[b] = pk[G * D + 2 * g];
+    lb[b] = pk[G * D + 2 * g + 1];
     ob[b] = pk[g * D + d];
   }
   const int pos = a.pos_dev ? *a.pos_dev : a.pos;
@@ -656,8 +613,8 @@ __global__ __launch_bounds__(kMergeThreads) void gqa_combine_kernel(DecodeArgs a
 #pragma unroll
       for (int b = 0; b < B; ++b) {
         const float* pk = base + static_cast<size_t>(min(k0 + b * NQ, nact - 1)) * PS;
-        mb[b] = pk[G * D + g];
-        lb[b] = pk[G * D + G + g];
+        mb[b] = pk[G * D + 2 * g];
+        lb[b] = pk[G * D + 2 * g + 1];
         ob[b] = pk[g * D + d];
       }
     }

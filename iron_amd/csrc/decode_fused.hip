@@ -351,7 +351,8 @@ __device__ __forceinline__ void publish_rows4(__amdgpu_buffer_rsrc_t r, int p0, 
 // (kv); the merged output is published as pairs.
 struct FusedDecodeIo {
   static constexpr bool kEarly = false;
-  static constexpr int kMergeLoads = 8;  // the persistent workgroup holds other stages' weights too
+  static constexpr bool kStaleL1 = true;   // a persistent workgroup may have merged earlier layers' partials
+  static constexpr int kMergeChunks = 8;   // the persistent workgroup holds other stages' weights too
   const FusedArgs& fa;
   int qkv_p0, att_p0;
   unsigned tag;
@@ -516,7 +517,7 @@ __device__ void loop_a(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag
     if (pos < 0) return;
     att = s * kDecChunk <= pos && pos < a.max_len && pos < a.angle_rows;
     if (att) kv = load_kv_rows<RES>(opaque_tid(), static_cast<const uint16_t*>(L0.k_cache), static_cast<const uint16_t*>(L0.v_cache),
-                                    a.max_len, s, j);
+                                    a.max_len, s * kDecChunk, j);
   }
   for (int l = 0; l < a.n_layers; ++l) {
     const IronDecodeLayer& L = a.layers[l];
@@ -557,7 +558,7 @@ __device__ void loop_a(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag
         d.nsplit = a.nsplit;
         d.scale_log2 = a.scale_log2;
         FusedDecodeIo io{a, base + kOffQkv, base + kOffAtt, tag, xs, flag, kv};
-        gqa_decode_chunk<kGQ, true, RES>(d, s, j, pos, io);  // always reaches its input wait (flag[2])
+        gqa_decode_chunk<kGQ, true, RES, 4>(d, s, j, pos, io);  // always reaches its input wait (flag[2])
         lds_barrier();
         if (flag[2]) return;  // that wait gave up (the status says so)
       }
@@ -587,7 +588,7 @@ __device__ void loop_a(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag
       gemv_fetch(wq, N.qkv_codes, N.qkv_scales, nullptr, nullptr, gw);
       if (att)
         kv = load_kv_rows<RES>(opaque_tid(), static_cast<const uint16_t*>(N.k_cache), static_cast<const uint16_t*>(N.v_cache),
-                               a.max_len, s, j);
+                               a.max_len, s * kDecChunk, j);
     }
     {
       uint16_t v[2];

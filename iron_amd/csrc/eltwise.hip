@@ -238,12 +238,12 @@ __global__ __launch_bounds__(kBlock) void rope_kernel(const uint16_t* __restrict
   uint16_t* orow = out + static_cast<size_t>(r) * cols;
   if (method == 0) {
     const float x1 = bf16_to_f32(xr[i]), x2 = bf16_to_f32(xr[i + half]);
-    orow[i] = f32_to_bf16(x1 * c - x2 * s);
-    orow[i + half] = f32_to_bf16(x2 * c + x1 * s);
+    orow[i] = f32_to_bf16(rot_sub(x1, c, x2, s));
+    orow[i + half] = f32_to_bf16(rot_add(x2, c, x1, s));
   } else {
     const float xe = bf16_to_f32(xr[2 * i]), xo = bf16_to_f32(xr[2 * i + 1]);
-    orow[2 * i] = f32_to_bf16(xe * c - xo * s);
-    orow[2 * i + 1] = f32_to_bf16(xe * s + xo * c);
+    orow[2 * i] = f32_to_bf16(rot_sub(xe, c, xo, s));
+    orow[2 * i + 1] = f32_to_bf16(rot_add(xe, s, xo, c));
   }
 }
 

@@ -16,6 +16,18 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;  // CDNA4 wavefront width
 
+// a b - c d and a b + c d with each product and the sum rounded to fp32 on
+// their own (no fused multiply-add, which HIP forms by default): the RoPE
+// rotation as the fp32 reference computes it, the same in every kernel.
+__device__ __forceinline__ float rot_sub(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+  return a * b - c * d;
+}
+__device__ __forceinline__ float rot_add(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+  return a * b + c * d;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }

@@ -147,7 +147,7 @@ __global__ __launch_bounds__(256) void qkv_scatter_kernel(const uint16_t* __rest
   if (h < H + Hkv) {
     const float c = angles[static_cast<size_t>(p) * D + 2 * i], sn = angles[static_cast<size_t>(p) * D + 2 * i + 1];
     const float x1 = val(i), x2 = val(i + 32);
-    const uint16_t y1 = f32_to_bf16(x1 * c - x2 * sn), y2 = f32_to_bf16(x2 * c + x1 * sn);
+    const uint16_t y1 = f32_to_bf16(rot_sub(x1, c, x2, sn)), y2 = f32_to_bf16(rot_add(x2, c, x1, sn));
     uint16_t* dst = h < H ? q_out + static_cast<size_t>(s) * H * D + h * D
                           : k_cache + (static_cast<size_t>(h - H) * max_len + p) * D;
     dst[i] = y1;

@@ -59,7 +59,7 @@ def test_config3_gqa_decode(gpu):
     assert torch.equal(kcd[:, pos], kref[:, pos]) and torch.equal(vcd[:, pos], vref[:, pos])
 
 
-@pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 127, 1000, 4095])
+@pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 127, 128, 129, 255, 1000, 4095])
 @pytest.mark.parametrize("use_tensor", [False, True])
 def test_gqa_decode_positions(gpu, pos, use_tensor):
     max_len = 4096
@@ -82,6 +82,27 @@ def test_gqa_decode_group_sizes(gpu, H, Hkv):
     max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
     assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
     assert torch.equal(kcd[:, pos], kref[:, pos]) and torch.equal(vcd[:, pos], vref[:, pos])
+
+
+# A long cache (max_len / 128 chunks x Hkv >= the CU count) takes 128-position
+# chunks of 8 waves on the one-launch path; every group size there, with
+# stale NaN rows past pos and a reused workspace (counters back at zero).
+@pytest.mark.parametrize("H,Hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (32, 16), (64, 32)])
+def test_gqa_decode_long_cache_group_sizes(gpu, H, Hkv):
+    max_len = 4224  # 33 chunks of 128 per KV head
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, L=max_len, seed=H + Hkv)
+    angles = ops.rope_angles_table(64, max_len)
+    op = None
+    for pos in (4223, 2049, 127, 4100):
+        ref, kref, vref = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+        out, kcd, vcd, op = _run_decode(gpu, q, kn, vn, kc, vc, pos, angles, max_len, op=op, fill=float("nan"))
+        assert torch.isfinite(out.float()).all(), pos
+        max_abs, rel_l2 = ops.max_abs_rel_l2(out, ref)
+        assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (pos, max_abs, rel_l2)
+        for name, got, want in (("k", kcd[:, pos], kref[:, pos]), ("v", vcd[:, pos], vref[:, pos])):
+            bad = (got.view(torch.int16) != want.view(torch.int16)).nonzero().tolist()
+            assert not bad, (pos, name, bad[:8], got.float().flatten()[:4].tolist(), want.float().flatten()[:4].tolist())
+        assert int(_counters(op, gpu).abs().sum()) == 0, pos
 
 
 @pytest.mark.parametrize("Hkv", [8, 2])
