@@ -196,9 +196,10 @@ long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_
 /* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}).
  * With n_kv_heads a multiple of 8, on a device whose workgroups with ids
  * congruent mod 8 run on one XCD (iron_xcd_round_robin), it is one kernel
- * launch after a one-wave counter reset (each KV head's chunks run on one XCD
- * and the last of them to finish merges them there); otherwise the chunk
- * partials, then a merge kernel:
+ * launch after a one-wave counter reset (each KV head's chunks of 64
+ * positions, or 128 when max_len / 128 x n_kv_heads reaches the device's CU
+ * count, run on one XCD, and the last of them to finish merges them there);
+ * otherwise 64-position chunk partials, then a merge kernel:
  *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
  *                                               (angle_rows, 64) [cos,sin])
  *   k_cache[:, pos] = k', v_cache[:, pos] = v_new
@@ -450,7 +451,11 @@ long long iron_llama_decode_fused_exchange_bytes(int n_layers);
  * the qkv GEMV (rms scale), the GQA attention of iron_gqa_decode_ex (RoPE,
  * cache append at the new position), o_proj + residual, the SwiGLU pair and
  * down + residual; x_out (2048 bf16) receives the last layer's output.
- * Results are bit-identical to those 82 separate launches. Stages hand their
+ * Results are bit-identical to those 82 separate launches while their
+ * attention splits the cache into 64-position chunks, as this step always does
+ * (max_len / 128 x 8 below the CU count: max_len < 4096 on MI355X); on longer
+ * caches the separate attention uses 128-position chunks and the two agree to
+ * fp32 rounding of the merge. Stages hand their
  * vectors over inside the launch through `exchange`
  * (iron_llama_decode_fused_exchange_bytes, 256-byte aligned, zero-filled once;
  * contents carry over between calls) tagged with *epoch, which must be
