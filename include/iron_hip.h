@@ -193,19 +193,30 @@ int iron_rope(const void* x, const void* angles, int angles_fp32, void* out, int
  * stream-ordered. */
 long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len);
 
+/* Positions per attention chunk (64 or 128) that iron_gqa_decode and its
+ * variants take for this shape at position (or hint) pos on this stream's
+ * device; -1 if the shape is invalid. The shape of a launch depends on the
+ * position, so a caller that captures decode steps into graphs with a device
+ * position captures one graph per shape and replays the one this returns for
+ * the position at hand. No reference counterpart: it describes a launch. */
+int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, void* stream);
+
 /* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}).
  * With n_kv_heads a multiple of 8, on a device whose workgroups with ids
  * congruent mod 8 run on one XCD (iron_xcd_round_robin), it is one kernel
- * launch after a one-wave counter reset (each KV head's chunks of 64
- * positions, or 128 when max_len / 128 x n_kv_heads reaches the device's CU
- * count, run on one XCD, and the last of them to finish merges them there);
- * otherwise 64-position chunk partials, then a merge kernel:
+ * launch after a one-wave counter reset (each KV head's chunks run on one
+ * XCD, and the last of them to finish merges them there; chunks of 64
+ * positions, or of 128 once the active 128-position chunks of all KV heads
+ * reach half the device's CUs: iron_gqa_decode_chunk_positions); otherwise
+ * 64-position chunk partials, then a merge kernel:
  *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
  *                                               (angle_rows, 64) [cos,sin])
  *   k_cache[:, pos] = k', v_cache[:, pos] = v_new
  *   out[h] = softmax(scale * q'[h] . K[h/G, 0..pos]) V[h/G, 0..pos]  (fp32)
  * q (H,64), k_new/v_new (Hkv,64), caches (Hkv,max_len,64), out (H,64) bf16.
- * pos_dev (device int32, may be NULL) overrides pos at run time.
+ * pos_dev (device int32, may be NULL) overrides pos at run time; pos is then
+ * a hint of the position the call will see (-1: none, taken as max_len - 1),
+ * used only to choose the launch shape: every value gives a correct result.
  * Replaces the decode attention runlist (RoPE, StridedCopy, Repeat, GEMV
  * scores, scale Mul, masked Softmax, Transpose, GEMV context) of
  * iron/applications/llama_3.2_1b/llama_npu.py:486-523 and the CPU golden

@@ -71,6 +71,7 @@ SIGNATURES: dict[str, list] = {
 # ... except these queries, which return a value.
 QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
+    "iron_gqa_decode_chunk_positions": (_I, [_I, _I, _I, _I, _I, _P]),
     "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
     "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
     "iron_xcd_round_robin": (_I, [_P]),

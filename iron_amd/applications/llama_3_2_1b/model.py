@@ -322,8 +322,8 @@ class LlamaHIP:
             self.exchange = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
             self.epoch = torch.ones(1, dtype=torch.int32, device=dev)
             self.status = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.graph = None
-        self.graph_multi = None
+        self.graph = None  # attention chunk positions -> one-step decode graph
+        self.graph_multi = None  # attention chunk positions -> DECODE_GRAPH_STEPS-step graph
         self._prefill_bufs = None  # activations of the longest prompt seen (see _pbufs)
         self._prefill_graphs = {}  # (prompt length, start position) -> captured prefill, least recently used first
         self._gemm_ws = torch.empty(0, dtype=torch.uint8, device=dev)
@@ -365,9 +365,29 @@ class LlamaHIP:
         self.pos.copy_(torch.zeros(1, dtype=torch.int32))
 
     # ------------------------------------------------------------ decode
-    def decode_step(self) -> None:
+    def _chunk_positions(self, pos: int) -> int:
+        """Positions per attention chunk the decode attention takes at `pos` (64
+        or 128: its launch shape, chosen from a position hint; 64 for the
+        one-launch step, whose attention is its own)."""
+        cfg = self.cfg
+        if self.fused:
+            return 64
+        return int(_lib.query("iron_gqa_decode_chunk_positions", cfg.n_heads, cfg.n_kv_groups, cfg.head_dim,
+                              cfg.max_seq_len, pos, self._stream()))
+
+    def _decode_shapes(self) -> dict:
+        """One position hint per attention launch shape the decode can take
+        (the shape depends on the position, which the graphs keep on the device)."""
+        shapes = {}
+        for p in (0, self.cfg.max_seq_len - 1):
+            shapes.setdefault(self._chunk_positions(p), p)
+        return shapes
+
+    def decode_step(self, pos_hint: int = -1) -> None:
         """Enqueue one decode step: the previous step's argmax keys pick the token
-        (pos advances), then the layers, then the head writes logits and keys."""
+        (pos advances), then the layers, then the head writes logits and keys.
+        pos_hint: the position the step is expected at (it picks the attention's
+        launch shape only; the position itself is read on the device)."""
         cfg, s = self.cfg, self._stream()
         Hd, q_rows, kv_rows = cfg.head_dim, cfg.n_heads * cfg.head_dim, cfg.n_kv_groups * cfg.head_dim
         if self.fused:
@@ -393,7 +413,7 @@ class LlamaHIP:
             L["qkv"].gemv(self.x, self.qkv, s, norm_scale=True, eps=cfg.eps)
             _lib.call("iron_gqa_decode_ex", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.k_cache[i].data_ptr(),
                       self.v_cache[i].data_ptr(), self.angles.data_ptr(), self.angles.shape[0], self.attn.data_ptr(),
-                      self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, 0,
+                      self.attn_ws.data_ptr(), cfg.n_heads, cfg.n_kv_groups, Hd, cfg.max_seq_len, pos_hint,
                       self.pos.data_ptr(), scale, self.kv_flags | COUNTERS_ZERO, s)
             L["o"].gemv(self.attn, self.x, s, residual=self.x)
             L["gate"].gemv(self.x, self.h, s, norm_scale=True, eps=cfg.eps, pair=L["up"])
@@ -429,8 +449,9 @@ class LlamaHIP:
         before any attention reads it; token and position are restored.
         """
         tok, pos, keys = self.token.clone(), self.pos.clone(), self.keys.clone()
-        self.pos.fill_(self.cfg.max_seq_len - 1)
-        self.decode_step()
+        for hint in self._decode_shapes().values():
+            self.pos.fill_(self.cfg.max_seq_len - 1)
+            self.decode_step(hint)
         self.token.copy_(tok)
         self.pos.copy_(pos)
         self.keys.copy_(keys)
@@ -443,11 +464,14 @@ class LlamaHIP:
 
     def capture_decode_graph(self) -> None:
         """Capture decode_step() as HIP graphs: one step, and DECODE_GRAPH_STEPS
-        steps back to back (the position advances on the device inside)."""
+        steps back to back (the position advances on the device inside), for
+        each attention launch shape the decode can take."""
         self._warmup()
-        self.graph = capture_graph(self.decode_step, self.device)
         k = self.DECODE_GRAPH_STEPS
-        self.graph_multi = capture_graph(lambda: [self.decode_step() for _ in range(k)], self.device)
+        self.graph, self.graph_multi = {}, {}
+        for shape, hint in self._decode_shapes().items():
+            self.graph[shape] = capture_graph(lambda: self.decode_step(hint), self.device)
+            self.graph_multi[shape] = capture_graph(lambda: [self.decode_step(hint) for _ in range(k)], self.device)
 
     def decode(self, n_steps: int, use_graph: bool = True) -> None:
         """Run n_steps greedy decode steps from the current token and position
@@ -457,17 +481,19 @@ class LlamaHIP:
                              f"{self.cfg.max_seq_len}")
         if use_graph and self.graph is None:
             self.capture_decode_graph()
-        left = n_steps
+        left, pos = n_steps, self.host_pos
         if use_graph:
             k = self.DECODE_GRAPH_STEPS
             while left >= k:
-                self.graph_multi.replay()
+                self.graph_multi[self._chunk_positions(pos + k // 2)].replay()
                 left -= k
+                pos += k
         for _ in range(left):
             if use_graph:
-                self.graph.replay()
+                self.graph[self._chunk_positions(pos)].replay()
             else:
-                self.decode_step()
+                self.decode_step(pos)
+            pos += 1
         self.host_pos += n_steps
         self.check_decode_status()
 

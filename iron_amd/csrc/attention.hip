@@ -402,6 +402,17 @@ static long long decode_head_stride(int G, int max_len) {
   return (static_cast<long long>(decode_nsplit(max_len)) * decode_part_stride(G) + 63) / 64 * 64;
 }
 
+static bool decode_long_chunks(int n_kv_heads, int max_len, int pos);
+
+extern "C" int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos,
+                                               void* stream) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim != kD || max_len <= 0) return -1;
+  const int G = n_heads / n_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
+  const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(static_cast<hipStream_t>(stream)) == 1;
+  return one && decode_long_chunks(n_kv_heads, max_len, pos) ? 16 * kDecWaves1 : kDecChunk;
+}
+
 extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len) {
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim != kD || max_len <= 0) return -1;
   const int G = n_heads / n_kv_heads;
@@ -429,15 +440,26 @@ static int device_cus() {
   return c;
 }
 
+// Whether the one-launch path takes 128-position chunks (kDecWaves1 waves) for
+// a call at position `pos` (the position, or with a device position the
+// caller's hint of it; -1: no hint, the cache's last slot): when the active
+// 128-position chunks of all KV heads reach half the CUs. Below that, more
+// and smaller chunks keep more CUs loading; above it, half the partials to
+// merge and half the waves to dispatch win (decode at KV 512 and 4096 in the
+// model measured each way). Any choice gives a correct result.
+static bool decode_long_chunks(int n_kv_heads, int max_len, int pos) {
+  const int p = pos < 0 || pos >= max_len ? max_len - 1 : pos;
+  return static_cast<long long>(p / (16 * kDecWaves1) + 1) * n_kv_heads * 2 >= device_cus();
+}
+
 template <int G, bool RES>
-static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_launch, hipStream_t s) {
+static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_launch, bool long_chunks, hipStream_t s) {
   const dim3 block(kDecThreads);
   if (one_launch) {
-    // 128-position chunks (kDecWaves1 waves) when the cache is long enough for
-    // one per CU, else 64; the workspace holds the 64-position partials either way
+    // the workspace holds the 64-position partials either way
     DecodeArgs b = a;
     b.nsplit = (a.max_len + 16 * kDecWaves1 - 1) / (16 * kDecWaves1);
-    if (b.nsplit * n_kv_heads >= device_cus())
+    if (long_chunks)
       IRON_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1>), dim3(b.nsplit * n_kv_heads), dim3(kDecWaves1 * kWave),
                   0, s, b);
     else
@@ -488,21 +510,22 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(s) == 1;
+  const bool long_chunks = one && decode_long_chunks(n_kv_heads, max_len, pos);
   if (one && !(flags & IRON_GQA_COUNTERS_ZERO))
     IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
   if (flags & IRON_GQA_KV_RESIDENT) {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, one, s); break;
-      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, one, s); break;
-      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, one, s); break;
-      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, one, s); break;
+      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, one, long_chunks, s); break;
+      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, one, long_chunks, s); break;
+      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, one, long_chunks, s); break;
+      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, one, long_chunks, s); break;
     }
   } else {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, one, s); break;
-      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, one, s); break;
-      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, one, s); break;
-      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, one, s); break;
+      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, one, long_chunks, s); break;
+      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, one, long_chunks, s); break;
+      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, one, long_chunks, s); break;
+      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, one, long_chunks, s); break;
     }
   }
   return check_launch(who);

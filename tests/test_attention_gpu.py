@@ -105,6 +105,37 @@ def test_gqa_decode_long_cache_group_sizes(gpu, H, Hkv):
         assert int(_counters(op, gpu).abs().sum()) == 0, pos
 
 
+def test_gqa_decode_position_hint_picks_the_shape(gpu):
+    """With a device position, the host position is a hint that picks the
+    launch shape (64- or 128-position chunks) and nothing else: both shapes
+    match the oracle at the same device position, and the shape query reports
+    what each hint picks (64 below half the CUs' worth of 128-position chunks,
+    128 above)."""
+    from iron_amd import _lib
+    max_len = 4224
+    s = _lib.stream_handle(gpu)
+    shape = lambda p: _lib.query("iron_gqa_decode_chunk_positions", 32, 8, 64, max_len, p, s)
+    assert shape(0) == 64 and shape(max_len - 1) == 128 and shape(-1) == 128
+    assert _lib.query("iron_gqa_decode_chunk_positions", 8, 2, 64, max_len, max_len - 1, s) == 64  # two launches
+    assert _lib.query("iron_gqa_decode_chunk_positions", 32, 2, 64, max_len, 0, s) == -1  # group of 16
+    assert _lib.query("iron_gqa_decode_chunk_positions", 32, 8, 32, max_len, 0, s) == -1
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(L=max_len, seed=21)
+    angles = ops.rope_angles_table(64, max_len)
+    from iron_amd.operators import GQADecode
+    for pos in (3000, 130):
+        ref, _, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+        for hint in (0, max_len - 1):
+            op = GQADecode(num_heads=32, num_kv_heads=8, head_dim=64, max_len=max_len, angle_rows=max_len)
+            op.set_position(hint)
+            op.position_tensor = torch.tensor([pos], dtype=torch.int32, device=gpu)
+            kcd, vcd = kc.to(gpu).contiguous(), vc.to(gpu).contiguous()
+            out = torch.empty(32, 64, dtype=BF16, device=gpu)
+            op.get_callable()(q.to(gpu), kn.to(gpu), vn.to(gpu), kcd, vcd, angles.to(gpu), out)
+            torch.cuda.synchronize()
+            max_abs, rel_l2 = ops.max_abs_rel_l2(out.cpu(), ref)
+            assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (pos, hint, max_abs, rel_l2)
+
+
 @pytest.mark.parametrize("Hkv", [8, 2])
 @pytest.mark.parametrize("fill", [float("nan"), float("inf")])
 @pytest.mark.parametrize("pos", [0, 70, 383])
