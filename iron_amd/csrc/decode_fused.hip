@@ -33,8 +33,10 @@
 //
 // Arithmetic. Each role computes exactly what the separate kernels compute
 // (the same int4 group products, DPP reductions, norm scale, SiLU and residual
-// order, and the shared decode attention body), so the step's logits are
-// bit-identical to the 82-launch step.
+// order, and the shared decode attention body with 64-position chunks), so
+// the step's logits are bit-identical to the 82-launch step wherever that
+// step's attention takes 64-position chunks too (on long caches it takes 128,
+// whose merge sums in another order).
 #include "iron_common.hpp"
 #include "i4_dot.hpp"
 #include "decode_attn.hpp"
