@@ -220,6 +220,13 @@ def test_mha_causal(gpu, seq_len, heads, kv):
         (4, 2, 300, 300, 0, 0),  # not causal
         (8, 1, 77, 130, 0, 0),  # not causal, Skv not a multiple of the 64-key block
         (2, 2, 129, 1000, 1, 871),  # ragged query tile, long visible prefix
+        # more heads and longer prompts: many query tiles per head, all CUs busy
+        (32, 8, 2048, 2048, 1, 0),  # causal, the long-prompt shape
+        (64, 8, 1100, 1100, 1, 0),  # causal, ragged last tile
+        (256, 32, 300, 700, 1, 400),  # a second chunk over the cache
+        (96, 8, 513, 1000, 0, 0),  # not causal, Skv not a multiple of the 64-key block
+        (128, 128, 257, 257, 0, 0),  # one query head per KV head
+        (256, 8, 1, 4096, 1, 4095),  # one query at the last cache slot
     ],
 )
 def test_attention_prefill_abi(gpu, H, Hkv, Sq, Skv, causal, q_offset):
