@@ -31,10 +31,10 @@
 // Rows past M or N load row M-1 or N-1 instead: they only feed outputs that
 // are never stored.
 //
-// One barrier per step, placed after the step's last MFMAs are issued: those
-// MFMAs run while the wave waits for the next stage's loads and reads its
-// first fragments. Fragments are double-buffered in registers across the four
-// 16-deep k-slices of a step.
+// One barrier per step, placed before the step's last k-slice's MFMAs: those
+// MFMAs run while the next step's first fragments are read (the gemm_nt
+// kernel). Fragments are double-buffered in registers across the four 16-deep
+// k-slices of a step.
 // Tile order is XCD-aware (tile_coords): workgroup b runs on XCD b % 8, and
 // the tiles an XCD runs share A row blocks and B column blocks in its L2.
 // Epilogue: round to bf16, then activation and clamp (the flm.GEMM order),
@@ -381,24 +381,30 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
     wait_loads_barrier<0>();
   read_frags(0, 0, 0);
 
-  for (int s = 0; s < nk; ++s) {
+  // One step; LAST: the range's last step (no barrier, no next fragments). The
+  // last step is peeled off so that the other steps' final k-slice has one
+  // path into its MFMAs, and the compiler's LDS waits there count exactly.
+  auto step = [&](int s, auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
     // the stage read in step s-1: every wave passed the barrier after its last read of it
     if (s + NS - 1 < nk) issue(s + NS - 1);
-    // The compiler waits for every outstanding LDS read (lgkmcnt(0)) before each
-    // k-slice's MFMAs, so how it interleaves the next slice's fragment reads with
-    // this slice's MFMAs sets how much LDS latency is exposed; its DS/MFMA
+    // How the compiler interleaves the next slice's fragment reads with this
+    // slice's MFMAs sets how much LDS latency is exposed; its DS/MFMA
     // interleave strategy 0 measured 2-4% faster on every shape than its default.
     __builtin_amdgcn_iglp_opt(0);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
       const int cur = kk & 1, nxt = cur ^ 1;
-      if (kk + 1 < BK / 16) read_frags(nxt, s % NS, kk + 1);
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
-      if (kk + 1 == BK / 16 && s + 1 < nk) {
+      if (kk + 1 < BK / 16) {
+        read_frags(nxt, s % NS, kk + 1);
+      } else if constexpr (!LAST) {
+        // The step's barrier comes before its last k-slice's MFMAs, so the next
+        // step's first fragment reads are in flight while those MFMAs run. This
+        // wave's reads of stage s % NS (which the next step's loads refill) have
+        // all returned: the last slice's fragments are waited for first, after
+        // the previous slice's MFMAs (the scheduling fence keeps them above it).
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         // steps s+2..min(s+NS-1, nk-1) may stay in flight
         if (s + NS - 1 < nk)
           wait_loads_barrier<PW * (NS - 2)>();
@@ -406,8 +412,15 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
           wait_loads_barrier<0>();
         read_frags(nxt, (s + 1) % NS, 0);
       }
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
     }
-  }
+  };
+  for (int s = 0; s + 1 < nk; ++s) step(s, std::false_type{});
+  step(nk - 1, std::true_type{});
 
   store_tile<T>(a, acc, smem, m0, n0, kb, wm, wn, lane, tid);
 }
