@@ -244,7 +244,7 @@ int iron_gqa_decode_ex(const void* q, const void* k_new, const void* v_new, void
 /* iron_gqa_decode without a workspace argument: the counters and partials go
  * to a scratch array the library holds in device memory, one per GPU, for the life of the
  * process (iron_gqa_decode_noalloc_max_bytes(), 4 MiB: at the Llama-3.2-1B
- * shape, 32/8 heads, up to max_len 31744). It allocates nothing, so callers
+ * shape, 32/8 heads, up to max_len 29056). It allocates nothing, so callers
  * that cannot allocate device memory (code under hipGraph capture, tight
  * serving loops, harnesses that forbid hipMalloc) can use it. Shapes whose
  * iron_gqa_decode_workspace_bytes() exceed the maximum are rejected

@@ -63,10 +63,13 @@ struct DecodeArgs {
 };
 
 // One chunk's partial: G x 64 unnormalised outputs, then (maximum, sum) of
-// each of the G heads as one 8-byte pair, padded to a whole number of 16-byte quads.
+// each of the G heads as one 8-byte pair, padded to a whole number of
+// 128-byte lines (head regions start on such a line too), so no two chunks'
+// partials share a cache line: a line of them that a CU's L1 holds was
+// written whole by one chunk on that CU.
 template <int G>
 constexpr int part_stride() {
-  return (G * kD + 2 * G + 3) / 4 * 4;
+  return (G * kD + 2 * G + 31) / 32 * 32;
 }
 
 // Workgroups are dispatched to the XCDs round-robin, so workgroups whose
@@ -220,8 +223,8 @@ __device__ __forceinline__ DecodeKv load_kv_rows(int tid, const uint16_t* k_cach
 template <int G>
 struct PlainDecodeIo {
   static constexpr bool kEarly = true;
-  static constexpr bool kStaleL1 = false;  // a kernel starts with its L1 invalidated
-  static constexpr int kMergeChunks = 16;   // merge loads in flight per lane
+  static constexpr bool kStaleL1 = false;  // a launch's L1 starts invalidated (see gqa_decode_chunk's merge)
+  static constexpr int kMergeChunks = 16;  // merge loads in flight per lane
   const DecodeArgs& a;
   __device__ __forceinline__ void new_kv(int j, int cq, uint4& kna, uint4& knb, uint4& vna, uint4& vnb) const {
     kna = *reinterpret_cast<const uint4*>(a.k_new + static_cast<size_t>(j) * kD + cq * 8);
@@ -462,6 +465,11 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     }
     __syncthreads();
     if (!last_s) return;
+    // An Io whose persistent workgroups merge again later (Io::kStaleL1) may
+    // hold lines of an earlier merge's partials in this CU's L1: an
+    // agent-scope invalidate first (~0.9 us, so not for a fresh launch, where
+    // the L1 starts invalidated and holds at most lines a chunk on this CU
+    // wrote whole: part_stride).
     if constexpr (Io::kStaleL1) asm volatile("buffer_inv sc1" ::: "memory");
     gqa_merge_heads<G, NW>(a, j, nact, tid, io);
   }
@@ -475,10 +483,8 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
 // all in flight together (B = 8 or 16 by the active count, capped by
 // Io::kMergeChunks; more chunks take more rounds). Each slice folds its chunks
 // with a running maximum and the four slices meet by permlane swaps: no LDS
-// and no barrier. The partials were written to the XCD's L2 by other CUs; a
-// kernel starts with its L1 invalidated and no CU reads a head's partials
-// before its merge, so plain loads see them (an Io whose persistent
-// workgroups merge again later invalidates its L1 first, Io::kStaleL1).
+// and no barrier. The partials were written to the XCD's L2 by other CUs
+// and are read with plain loads (see the caller on this CU's L1).
 // Every sum runs in a fixed order: the result depends only on the data.
 template <int G, int NW, class Io>
 __device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, const Io& io) {

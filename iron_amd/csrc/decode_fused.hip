@@ -353,8 +353,8 @@ __device__ __forceinline__ void publish_rows4(__amdgpu_buffer_rsrc_t r, int p0, 
 // (kv); the merged output is published as pairs.
 struct FusedDecodeIo {
   static constexpr bool kEarly = false;
-  static constexpr bool kStaleL1 = true;   // a persistent workgroup may have merged earlier layers' partials
-  static constexpr int kMergeChunks = 8;   // the persistent workgroup holds other stages' weights too
+  static constexpr bool kStaleL1 = true;  // a persistent workgroup may have merged earlier layers' partials
+  static constexpr int kMergeChunks = 8;  // the persistent workgroup holds other stages' weights too
   const FusedArgs& fa;
   int qkv_p0, att_p0;
   unsigned tag;

@@ -103,8 +103,8 @@ def test_gqa_decode_noalloc_rejects_oversized_shape_on_host():
 
     cap = _lib.query("iron_gqa_decode_noalloc_max_bytes")
     assert cap == 4 << 20
-    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 31744) <= cap
-    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 31745) > cap
+    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 29056) <= cap
+    assert _lib.query("iron_gqa_decode_workspace_bytes", 32, 8, 64, 29057) > cap
     with pytest.raises(_lib.IronHipError, match="more than the 4194304"):
         _lib.call("iron_gqa_decode_noalloc", 16, 16, 16, 16, 16, 16, 32768, 16, 32, 8, 64, 32768, 0, None, 0.125,
                   None)
