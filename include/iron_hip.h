@@ -217,6 +217,9 @@ int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, i
  * pos_dev (device int32, may be NULL) overrides pos at run time; pos is then
  * a hint of the position the call will see (-1: none, taken as max_len - 1),
  * used only to choose the launch shape: every value gives a correct result.
+ * A device position outside [0, min(max_len, angle_rows)) cannot be refused
+ * before the launch: the call then changes nothing (out, the caches and the
+ * workspace's counters keep their contents).
  * Replaces the decode attention runlist (RoPE, StridedCopy, Repeat, GEMV
  * scores, scale Mul, masked Softmax, Transpose, GEMV context) of
  * iron/applications/llama_3.2_1b/llama_npu.py:486-523 and the CPU golden

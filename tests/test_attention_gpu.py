@@ -105,6 +105,38 @@ def test_gqa_decode_long_cache_group_sizes(gpu, H, Hkv):
         assert int(_counters(op, gpu).abs().sum()) == 0, pos
 
 
+@pytest.mark.parametrize("Hkv,max_len", [(8, 512), (8, 4224), (2, 512)])
+def test_gqa_decode_device_position_out_of_range_changes_nothing(gpu, Hkv, max_len):
+    """A device position outside the cache cannot be refused on the host: the
+    call leaves the output, the caches and the counters as they were, on every
+    launch path, and the next call with a valid position is exact."""
+    from iron_amd.operators import GQADecode
+
+    H = 4 * Hkv
+    q, kn, vn, kc, vc, _, _ = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, L=max_len, seed=Hkv + max_len)
+    angles = ops.rope_angles_table(64, max_len)
+    op = GQADecode(num_heads=H, num_kv_heads=Hkv, head_dim=64, max_len=max_len, angle_rows=max_len)
+    kcd, vcd = kc.to(gpu).contiguous(), vc.to(gpu).contiguous()
+    k0, v0 = kcd.clone(), vcd.clone()
+    out = torch.full((H, 64), 3.0, dtype=BF16, device=gpu)
+    fn = op.get_callable()
+    for bad in (max_len, max_len + 1000, -1):
+        op.position_tensor = torch.tensor([bad], dtype=torch.int32, device=gpu)
+        fn(q.to(gpu), kn.to(gpu), vn.to(gpu), kcd, vcd, angles.to(gpu), out)
+        torch.cuda.synchronize()
+        assert torch.all(out == 3.0), bad
+        assert torch.equal(kcd, k0) and torch.equal(vcd, v0), bad
+        assert int(_counters(op, gpu).abs().sum()) == 0, bad
+    pos = max_len - 1
+    op.position_tensor = torch.tensor([pos], dtype=torch.int32, device=gpu)
+    fn(q.to(gpu), kn.to(gpu), vn.to(gpu), kcd, vcd, angles.to(gpu), out)
+    torch.cuda.synchronize()
+    ref, kref, _ = ops.gqa_decode_reference(q, kn, vn, kc, vc, pos, angles)
+    max_abs, rel_l2 = ops.max_abs_rel_l2(out.cpu(), ref)
+    assert max_abs <= 2e-2 and rel_l2 <= 1e-2, (max_abs, rel_l2)
+    assert torch.equal(kcd[:, pos].cpu(), kref[:, pos])
+
+
 def test_gqa_decode_position_hint_picks_the_shape(gpu):
     """With a device position, the host position is a hint that picks the
     launch shape (64- or 128-position chunks) and nothing else: both shapes
