@@ -159,6 +159,90 @@ __global__ __launch_bounds__(256) void qkv_scatter_kernel(const uint16_t* __rest
   }
 }
 
+// The same scatter with 16-byte accesses: one thread per 8 rotated pairs,
+// dims 8 g .. 8 g + 7 and 32 + the same of one head of one row (g = 0..3),
+// the table's 16 floats [cos, sin] x 8 of those pairs in four 16-byte loads.
+// Every element takes the arithmetic of qkv_scatter_kernel (the split-K sum
+// in range order, rot_sub / rot_add, one bf16 rounding), so the two kernels
+// write identical bits. Used when every operand is 16-byte aligned.
+template <bool PART>
+__global__ __launch_bounds__(256) void qkv_scatter8_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ angles,
+                                                           uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_cache,
+                                                           uint16_t* __restrict__ v_cache, int S, int H, int Hkv,
+                                                           int max_len, int pos0, const float* __restrict__ part,
+                                                           int splits) {
+  constexpr int D = 64;
+  const int heads = H + 2 * Hkv;
+  const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= static_cast<long long>(S) * heads * 4) return;
+  const int s = static_cast<int>(t / (heads * 4));
+  const int rem = static_cast<int>(t % (heads * 4));
+  const int h = rem >> 2, i0 = (rem & 3) * 8;
+  const int p = pos0 + s;
+  const size_t off = static_cast<size_t>(s) * heads * D + h * D;
+  float x1[8], x2[8];  // dims i0 + e and i0 + 32 + e
+  if (PART) {
+    const size_t range = static_cast<size_t>(S) * heads * D;
+    float r1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, r2[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < splits; ++kb) {
+      const float4* pa = reinterpret_cast<const float4*>(part + kb * range + off + i0);
+      const float4* pb = reinterpret_cast<const float4*>(part + kb * range + off + i0 + 32);
+      const float4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
+      r1[0] += a0.x; r1[1] += a0.y; r1[2] += a0.z; r1[3] += a0.w;
+      r1[4] += a1.x; r1[5] += a1.y; r1[6] += a1.z; r1[7] += a1.w;
+      r2[0] += b0.x; r2[1] += b0.y; r2[2] += b0.z; r2[3] += b0.w;
+      r2[4] += b1.x; r2[5] += b1.y; r2[6] += b1.z; r2[7] += b1.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x1[e] = bf16_to_f32(f32_to_bf16(r1[e]));
+      x2[e] = bf16_to_f32(f32_to_bf16(r2[e]));
+    }
+  } else {
+    const uint4 a = *reinterpret_cast<const uint4*>(qkv + off + i0);
+    const uint4 b = *reinterpret_cast<const uint4*>(qkv + off + i0 + 32);
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x1[2 * e] = lo_bf16(wa[e]);
+      x1[2 * e + 1] = hi_bf16(wa[e]);
+      x2[2 * e] = lo_bf16(wb[e]);
+      x2[2 * e + 1] = hi_bf16(wb[e]);
+    }
+  }
+  uint32_t y1[4], y2[4];
+  uint16_t* dst;
+  if (h < H + Hkv) {
+    const float4* ap = reinterpret_cast<const float4*>(angles + static_cast<size_t>(p) * D + 2 * i0);
+    float ang[16];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float4 q = ap[u];
+      ang[4 * u] = q.x;
+      ang[4 * u + 1] = q.y;
+      ang[4 * u + 2] = q.z;
+      ang[4 * u + 3] = q.w;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c0 = ang[4 * e], s0 = ang[4 * e + 1], c1 = ang[4 * e + 2], s1 = ang[4 * e + 3];
+      y1[e] = pack_bf16x2(rot_sub(x1[2 * e], c0, x2[2 * e], s0), rot_sub(x1[2 * e + 1], c1, x2[2 * e + 1], s1));
+      y2[e] = pack_bf16x2(rot_add(x2[2 * e], c0, x1[2 * e], s0), rot_add(x2[2 * e + 1], c1, x1[2 * e + 1], s1));
+    }
+    dst = h < H ? q_out + static_cast<size_t>(s) * H * D + h * D
+                : k_cache + (static_cast<size_t>(h - H) * max_len + p) * D;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // exact: bf16 values (or the partial sums rounded once above)
+      y1[e] = pack_bf16x2(x1[2 * e], x1[2 * e + 1]);
+      y2[e] = pack_bf16x2(x2[2 * e], x2[2 * e + 1]);
+    }
+    dst = v_cache + (static_cast<size_t>(h - H - Hkv) * max_len + p) * D;
+  }
+  *reinterpret_cast<uint4*>(dst + i0) = make_uint4(y1[0], y1[1], y1[2], y1[3]);
+  *reinterpret_cast<uint4*>(dst + i0 + 32) = make_uint4(y2[0], y2[1], y2[2], y2[3]);
+}
+
 }  // namespace
 }  // namespace iron
 
@@ -207,11 +291,18 @@ extern "C" int iron_qkv_rope_scatter(const void* qkv, const float* angles, int a
   IRON_REQUIRE(pos0 >= 0 && pos0 + seq <= max_len && pos0 + seq <= angle_rows,
                "iron_qkv_rope_scatter: positions [%d, %d) exceed the cache (%d) or angle table (%d)", pos0,
                pos0 + seq, max_len, angle_rows);
-  const long long threads = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
-  IRON_LAUNCH(qkv_scatter_kernel<false>, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), angles,
-                     static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache),
-                     seq, n_heads, n_kv_heads, max_len, pos0, nullptr, 0);
+  const long long pairs = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
+  if (aligned16(qkv) && aligned16(angles) && aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache)) {
+    IRON_LAUNCH(qkv_scatter8_kernel<false>, dim3(static_cast<unsigned>((pairs / 8 + 255) / 256)), dim3(256), 0,
+                static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), angles,
+                static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq,
+                n_heads, n_kv_heads, max_len, pos0, nullptr, 0);
+  } else {
+    IRON_LAUNCH(qkv_scatter_kernel<false>, dim3(static_cast<unsigned>((pairs + 255) / 256)), dim3(256), 0,
+                static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(qkv), angles,
+                static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq,
+                n_heads, n_kv_heads, max_len, pos0, nullptr, 0);
+  }
   return check_launch("qkv_rope_scatter");
 }
 
@@ -225,10 +316,17 @@ extern "C" int iron_qkv_rope_scatter_splitk(const float* partial, int splits, co
   IRON_REQUIRE(pos0 >= 0 && pos0 + seq <= max_len && pos0 + seq <= angle_rows,
                "iron_qkv_rope_scatter_splitk: positions [%d, %d) exceed the cache (%d) or angle table (%d)", pos0,
                pos0 + seq, max_len, angle_rows);
-  const long long threads = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
-  IRON_LAUNCH(qkv_scatter_kernel<true>, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-              static_cast<hipStream_t>(stream), nullptr, angles, static_cast<uint16_t*>(q_out),
-              static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq, n_heads, n_kv_heads, max_len, pos0,
-              partial, splits);
+  const long long pairs = static_cast<long long>(seq) * (n_heads + 2 * n_kv_heads) * 32;
+  if (aligned16(partial) && aligned16(angles) && aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache)) {
+    IRON_LAUNCH(qkv_scatter8_kernel<true>, dim3(static_cast<unsigned>((pairs / 8 + 255) / 256)), dim3(256), 0,
+                static_cast<hipStream_t>(stream), nullptr, angles, static_cast<uint16_t*>(q_out),
+                static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq, n_heads, n_kv_heads, max_len,
+                pos0, partial, splits);
+  } else {
+    IRON_LAUNCH(qkv_scatter_kernel<true>, dim3(static_cast<unsigned>((pairs + 255) / 256)), dim3(256), 0,
+                static_cast<hipStream_t>(stream), nullptr, angles, static_cast<uint16_t*>(q_out),
+                static_cast<uint16_t*>(k_cache), static_cast<uint16_t*>(v_cache), seq, n_heads, n_kv_heads, max_len,
+                pos0, partial, splits);
+  }
   return check_launch("qkv_rope_scatter_splitk");
 }

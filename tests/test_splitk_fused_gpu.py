@@ -106,3 +106,64 @@ def test_qkv_scatter_splitk_matches_unfused(gpu, S, H, Hkv, K, splits, pos0, int
         assert not ops.within_bf16_ulps(kc[j, pos0:pos0 + S], ref.float(), n_ulp=1.0, atol=1e-6)
         assert torch.equal(vc[j, pos0:pos0 + S], Cc[:, H + Hkv + j])
         assert not kc[j, :pos0].any() and not kc[j, pos0 + S:].any()
+
+
+@pytest.mark.parametrize("S,H,Hkv,splits,pos0", [(100, 4, 2, 2, 3), (33, 32, 8, 4, 0), (7, 8, 1, 1, 600)])
+def test_qkv_scatter_vector_and_scalar_paths_agree(gpu, S, H, Hkv, splits, pos0):
+    """The scatter's 16-byte path (every operand 16-byte aligned) and its
+    element path (an operand that is not) write identical bits, from a bf16
+    qkv and from split-K partials."""
+    from iron_amd import _lib
+
+    print(f"qkv_scatter paths S={S} H={H} Hkv={Hkv} splits={splits} pos0={pos0}", flush=True)
+    D, max_len = 64, 640
+    N = (H + 2 * Hkv) * D
+    g = torch.Generator().manual_seed(S * 3 + H + splits)
+    qkv = torch.randn(S * N, generator=g).to(BF16)
+    part = torch.randn(splits * S * N, generator=g) * 0.3
+    angles = ops.rope_angles_table(D, max_len).to(gpu)
+    # copies at an offset of one element: 2 bytes (bf16) and 4 bytes (fp32) past a 16-byte boundary
+    qkv_a = qkv.to(gpu)
+    qkv_u = torch.zeros(S * N + 8, dtype=BF16, device=gpu)
+    qkv_u[1:1 + S * N] = qkv_a
+    part_a = part.to(gpu)
+    part_u = torch.zeros(splits * S * N + 4, device=gpu)
+    part_u[1:1 + splits * S * N] = part_a
+    s = _lib.stream_handle(gpu)
+    outs = {}
+    for name, src, split in (("bf16 aligned", qkv_a.data_ptr(), 0), ("bf16 offset", qkv_u[1:].data_ptr(), 0),
+                             ("partials aligned", part_a.data_ptr(), splits),
+                             ("partials offset", part_u[1:].data_ptr(), splits)):
+        q = torch.zeros(S, H * D, dtype=BF16, device=gpu)
+        kc = torch.zeros(Hkv, max_len, D, dtype=BF16, device=gpu)
+        vc = torch.zeros(Hkv, max_len, D, dtype=BF16, device=gpu)
+        tail = (angles.data_ptr(), max_len, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), S, H, Hkv, D, max_len, pos0, s)
+        if split:
+            _lib.call("iron_qkv_rope_scatter_splitk", src, split, *tail)
+        else:
+            _lib.call("iron_qkv_rope_scatter", src, *tail)
+        outs[name] = (q, kc, vc)
+    torch.cuda.synchronize()
+    for a, b in (("bf16 aligned", "bf16 offset"), ("partials aligned", "partials offset")):
+        for x, y in zip(outs[a], outs[b]):
+            assert torch.equal(x, y), (a, b)
+    # the bf16 path against the oracle's RoPE; v rows copied exactly
+    q, kc, vc = (t.cpu() for t in outs["bf16 aligned"])
+    rows = qkv.reshape(S, H + 2 * Hkv, D)
+    ang = angles.cpu()[pos0:pos0 + S]
+    for h in range(H):
+        ref = ops.rope_reference(rows[:, h], ang)
+        assert not ops.within_bf16_ulps(q.reshape(S, H, D)[:, h], ref.float(), n_ulp=1.0, atol=1e-6)
+    for j in range(Hkv):
+        ref = ops.rope_reference(rows[:, H + j], ang)
+        assert not ops.within_bf16_ulps(kc[j, pos0:pos0 + S], ref.float(), n_ulp=1.0, atol=1e-6)
+        assert torch.equal(vc[j, pos0:pos0 + S], rows[:, H + Hkv + j])
+    # the partials path: the v rows are the partial sums in range order, rounded once
+    vsum = part.reshape(splits, S, H + 2 * Hkv, D).sum(0) if splits > 1 else part.reshape(S, H + 2 * Hkv, D)
+    vc_p = outs["partials aligned"][2].cpu()
+    for j in range(Hkv):
+        exact = torch.zeros(S, D)
+        for kb in range(splits):
+            exact = exact + part.reshape(splits, S, H + 2 * Hkv, D)[kb, :, H + Hkv + j]
+        assert torch.equal(vc_p[j, pos0:pos0 + S], exact.to(BF16))
+        assert torch.allclose(exact, vsum[:, H + Hkv + j], atol=1e-5)
