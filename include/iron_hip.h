@@ -300,7 +300,8 @@ int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K
  * partial sums to `workspace` (splits*M*N*4 bytes, 16-byte aligned), and a
  * second kernel sums them in order and applies the same bf16 rounding,
  * epilogue and clamp. Deterministic. iron_gemm_splitk_choose returns the
- * split count this library uses for (M, N, K) (1: no split);
+ * split count this library uses for (M, N, K) with bf16 B (1: no split: the
+ * plain kernel's smaller tiles are faster unless K is long);
  * iron_gemm_splitk_workspace_bytes the workspace it needs. */
 int iron_gemm_splitk_choose(int M, int N, int K);
 long long iron_gemm_splitk_workspace_bytes(int M, int N, int splits);
@@ -327,13 +328,17 @@ int iron_gemm_bf16_nt_swiglu(const void* A, const void* Bgu, void* H, int M, int
  * iron_gemm_bf16_nt on them. codes (N, K/2) 16-byte aligned, scales
  * (N, K/32) 4-byte aligned, K % 64 == 0. splits > 1 splits K as
  * iron_gemm_bf16_nt_splitk does (workspace of splits*M*N*4 bytes; unused
- * when splits == 1). No reference counterpart as one operator: it is
+ * when splits == 1); iron_gemm_i4g32_splitk_choose returns the split count
+ * this library uses for (M, N, K) with int4-g32 B (its tiles are 128x128 or
+ * larger, so it splits shorter K than the bf16 policy). No reference
+ * counterpart as one operator: it is
  * Dequant (iron/operators/dequant/op.py:20-81) feeding flm.GEMM / GEMM
  * (iron/operators/flm/gemm/op.py:64-499, iron/operators/gemm/op.py:21-231)
  * without the bf16 round trip through memory. */
 int iron_gemm_i4g32_nt(const void* A, const void* codes, const void* scales, void* C, int M, int N, int K,
                        long long ldc, int epilogue, int has_clamp, float clamp_lo, float clamp_hi, int is_signed,
                        int splits, void* workspace, long long workspace_bytes, void* stream);
+int iron_gemm_i4g32_splitk_choose(int M, int N, int K);
 
 /* First pass of the split-K GEMMs alone, for a consumer that merges the
  * partial sums itself (iron_rmsnorm_splitk, iron_qkv_rope_scatter_splitk):

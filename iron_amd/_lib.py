@@ -76,6 +76,7 @@ QUERIES: dict[str, tuple] = {
     "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
     "iron_xcd_round_robin": (_I, [_P]),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
+    "iron_gemm_i4g32_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_splitk_workspace_bytes": (_LL, [_I, _I, _I]),
     "iron_probe_read_workgroups": (_LL, [_LL, _I]),
 }

@@ -197,11 +197,17 @@ class Linear:
                       x.data_ptr(), y.data_ptr(), self.N, self.K, mode, None, float(eps), _lib.ptr(residual), 0,
                       _lib.ptr(keys), stream)
 
+    def _splits(self, rows):
+        """The library's K split for this projection at `rows` rows: the bf16
+        policy for a bf16 copy, the int4-g32 one when the GEMM reads the codes."""
+        q = "iron_gemm_splitk_choose" if self._bf16 is not None else "iron_gemm_i4g32_splitk_choose"
+        return _lib.query(q, rows, self.N, self.K)
+
     def gemm(self, X, Y, rows, stream, workspace=None):
         """Y (rows, N) = X (rows, K) . W^T on bf16 MFMA; split over K (fp32
         partials in ``workspace(nbytes)``) when the output tiles alone cannot
         fill the GPU. Reads the int4 weights directly when no bf16 copy is kept."""
-        splits = _lib.query("iron_gemm_splitk_choose", rows, self.N, self.K) if workspace is not None else 1
+        splits = self._splits(rows) if workspace is not None else 1
         need, ws = 0, None
         if splits > 1:
             need = int(_lib.query("iron_gemm_splitk_workspace_bytes", rows, self.N, splits))
@@ -222,7 +228,7 @@ class Linear:
         (splits, rows, N) in ``workspace(nbytes)``, for a consumer that merges
         them (iron_rmsnorm_splitk, iron_qkv_rope_scatter_splitk). Returns
         (partials, splits), or None when this shape is not split (use gemm)."""
-        splits = _lib.query("iron_gemm_splitk_choose", rows, self.N, self.K)
+        splits = self._splits(rows)
         if splits < 2:
             return None
         need = int(_lib.query("iron_gemm_splitk_workspace_bytes", rows, self.N, splits))

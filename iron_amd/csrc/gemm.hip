@@ -803,14 +803,56 @@ extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, i
   return check_launch("gemm_bf16_nt");
 }
 
-extern "C" int iron_gemm_splitk_choose(int M, int N, int K) {
-  // Split K while the workgroups stay within 1.25x the 256 CUs and every K range
-  // keeps >= 8 steps of 64; at most 8 ranges.
-  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 1;
+// Split-K policies, measured (graph replays with cold weights over M =
+// 128..2048 for (N, K) = (2048, 2048), (3072, 2048), (2048, 8192), and the
+// Llama prefill at 512 tokens).
+//
+// int4-g32 (iron_gemm_i4g32_nt, whose tiles are 128x128 or larger): split K
+// while the workgroups stay within 1.25x the 256 CUs and every range keeps
+// >= 8 steps of 64, at most 8 ranges (512x2048->2048: 28.7 us plain, 23.3 in
+// 4 ranges; 512x2048->3072: 29.3 plain, 27.4 in 2).
+static int splitk_short(int M, int N, int K) {
   const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile);
   int s = 1;
   while (s < 8 && tiles * s * 2 <= 320 && (K / BK) % (s * 2) == 0 && K / BK / (s * 2) >= 8) s *= 2;
   return s;
+}
+
+// Workgroups of the plain bf16 GEMM (gemm_launch's choice for grids that
+// 128x128 tiles leave idle: 64x64 or 128x64 tiles, at most one per CU).
+static long long plain_small_grid(int M, int N) {
+  auto tiles = [&](int bm, int bn) { return static_cast<long long>((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (tiles(128, 128) < 256) {
+    if (tiles(64, 64) <= 256) return tiles(64, 64);
+    if (tiles(128, 64) <= 256) return tiles(128, 64);
+  }
+  return tiles(128, 128);
+}
+
+// bf16: a K of fewer than 64 steps is split only when the plain kernel's
+// tiles leave CUs idle, and then as the int4 policy does (prefill at 512
+// tokens: o_proj, 256 tiles of 64x64, runs unsplit: 12.4 us against 20.5 in
+// 4 ranges; qkv, 192 tiles of 128x64, keeps 2 ranges: TTFT 2.05-2.08 ms with
+// both split, 2.02-2.05 with neither, 1.99-2.03 so). A long K is split into
+// ranges of >= 32 steps, or >= 16 while the workgroups fit one per CU, with
+// at most 512 workgroups (K 8192: M 128 and 256 -> 8 ranges, 512 and 1024 ->
+// 4, 2048 -> 2; 512x8192->2048: 41.7 us plain, 32.1 in 4).
+extern "C" int iron_gemm_splitk_choose(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 1;
+  if (K / BK < 64) return plain_small_grid(M, N) >= 256 ? 1 : splitk_short(M, N, K);
+  const long long tiles = static_cast<long long>((M + kSplitTile - 1) / kSplitTile) * ((N + kSplitTile - 1) / kSplitTile);
+  int best = 1;
+  for (int s = 2; s <= 8; s *= 2) {
+    const int steps = K / BK / s;
+    if ((K / BK) % s || tiles * s > 512) break;
+    if (steps >= 32 || (steps >= 16 && tiles * s <= 256)) best = s;
+  }
+  return best;
+}
+
+extern "C" int iron_gemm_i4g32_splitk_choose(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % BK) return 1;
+  return splitk_short(M, N, K);
 }
 
 extern "C" long long iron_gemm_splitk_workspace_bytes(int M, int N, int splits) {

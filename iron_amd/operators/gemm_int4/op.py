@@ -49,7 +49,7 @@ class GEMMInt4(HIPOperator):
         ]
 
     def _launch(self, A, codes, scales, C, *, stream):
-        splits = _lib.query("iron_gemm_splitk_choose", self.M, self.N, self.K)
+        splits = _lib.query("iron_gemm_i4g32_splitk_choose", self.M, self.N, self.K)
         ws, need = None, 0
         if splits > 1:
             need = int(_lib.query("iron_gemm_splitk_workspace_bytes", self.M, self.N, splits))

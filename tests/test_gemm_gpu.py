@@ -169,9 +169,19 @@ def test_gemm_splitk(gpu, M, K, N, splits, epi, clamp):
 def test_gemm_splitk_choice_and_errors(gpu):
     from iron_amd import _lib
 
+    # bf16: a short K is split only when the plain kernel's 64x64 / 128x64 tiles leave CUs idle
     assert _lib.query("iron_gemm_splitk_choose", 512, 2048, 8192) == 4
-    assert _lib.query("iron_gemm_splitk_choose", 512, 8192, 2048) == 1  # 256 tiles already fill the GPU
+    assert _lib.query("iron_gemm_splitk_choose", 128, 2048, 8192) == 8
+    assert _lib.query("iron_gemm_splitk_choose", 2048, 2048, 8192) == 2
+    assert _lib.query("iron_gemm_splitk_choose", 512, 2048, 2048) == 1  # 256 tiles of 64x64
+    assert _lib.query("iron_gemm_splitk_choose", 512, 3072, 2048) == 2  # 192 tiles of 128x64
+    assert _lib.query("iron_gemm_splitk_choose", 512, 8192, 2048) == 1
     assert _lib.query("iron_gemm_splitk_choose", 4096, 4096, 4096) == 1
+    # int4-g32: 128x128 tiles or larger, so shorter K is split too
+    assert _lib.query("iron_gemm_i4g32_splitk_choose", 512, 2048, 2048) == 4
+    assert _lib.query("iron_gemm_i4g32_splitk_choose", 512, 3072, 2048) == 2
+    assert _lib.query("iron_gemm_i4g32_splitk_choose", 512, 2048, 8192) == 4
+    assert _lib.query("iron_gemm_i4g32_splitk_choose", 512, 8192, 2048) == 1  # 256 tiles already fill the GPU
     A = torch.zeros(128, 192, dtype=BF16, device=gpu)
     C = torch.zeros(128, 128, dtype=BF16, device=gpu)
     with pytest.raises(_lib.IronHipError, match="must divide"):
@@ -209,7 +219,7 @@ def test_gemm_i4g32_matches_bf16_on_dequantized(gpu, M, K, N, signed):
     A = torch.randn(M, K, generator=gen).to(BF16)
     W = ops.dequant_planar(codes, scales, signed=signed)
     s = _lib.stream_handle(gpu)
-    splits = _lib.query("iron_gemm_splitk_choose", M, N, K)
+    splits = _lib.query("iron_gemm_i4g32_splitk_choose", M, N, K)
     need = int(_lib.query("iron_gemm_splitk_workspace_bytes", M, N, splits))
     ws = torch.empty(max(need, 16), dtype=torch.uint8, device=gpu)
     Ad, Wd, cd, sd = A.to(gpu), W.to(gpu), codes.to(gpu), scales.to(gpu)
@@ -230,8 +240,10 @@ def test_gemm_i4g32_matches_bf16_on_dequantized(gpu, M, K, N, signed):
 
 
 def test_gemm_int4_operator_epilogue_and_errors(gpu):
-    """GEMMInt4 operator (arg order A, codes, scales, C) against GEMM on the
-    dequantized weights; the flm epilogue path of the C ABI; argument checks."""
+    """GEMMInt4 operator (arg order A, codes, scales, C) against the GEMM
+    operator and the split-K bf16 GEMM on the dequantized weights (both
+    policies split this K in 2 ranges: bit-identical); the flm epilogue path
+    of the C ABI; argument checks."""
     from iron_amd import _lib
     from iron_amd.operators import GEMM, GEMMInt4
 
@@ -244,11 +256,19 @@ def test_gemm_int4_operator_epilogue_and_errors(gpu):
     Ad, Wd, cd, sd = A.to(gpu), W.to(gpu), codes.to(gpu), scales.to(gpu)
     C4 = torch.empty(M, N, dtype=BF16, device=gpu)
     Cb = torch.empty(M, N, dtype=BF16, device=gpu)
+    Cs = torch.empty(M, N, dtype=BF16, device=gpu)
+    s = _lib.stream_handle(gpu)
+    splits = _lib.query("iron_gemm_i4g32_splitk_choose", M, N, K)
+    assert splits == 2 and _lib.query("iron_gemm_splitk_choose", M, N, K) == 2  # 48 tiles of 64x64
+    need = int(_lib.query("iron_gemm_splitk_workspace_bytes", M, N, splits))
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
     GEMMInt4(M=M, K=K, N=N).get_callable()(Ad, cd, sd, C4)
     GEMM(M=M, K=K, N=N, b_col_maj=True).get_callable()(Ad, Wd, Cb)
+    _lib.call("iron_gemm_bf16_nt_splitk", Ad.data_ptr(), Wd.data_ptr(), Cs.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0,
+              splits, ws.data_ptr(), need, s)
     torch.cuda.synchronize()
+    assert torch.equal(C4.cpu().view(torch.int16), Cs.cpu().view(torch.int16))
     assert torch.equal(C4.cpu().view(torch.int16), Cb.cpu().view(torch.int16))
-    s = _lib.stream_handle(gpu)
     _lib.call("iron_gemm_i4g32_nt", Ad.data_ptr(), cd.data_ptr(), sd.data_ptr(), C4.data_ptr(), M, N, K, N, 2, 1,
               -1.0, 1.5, 1, 1, None, 0, s)
     _lib.call("iron_gemm_bf16_nt", Ad.data_ptr(), Wd.data_ptr(), Cb.data_ptr(), M, N, K, N, 2, 1, -1.0, 1.5, s)

@@ -153,9 +153,11 @@ def test_prefill_fused_merge_bit_identical(gpu, prefill_int4):
     from iron_amd.applications.llama_3_2_1b import LlamaConfig, LlamaHIP, random_weights
 
     cfg = LlamaConfig(prefill_int4=prefill_int4, **MID)
-    # at these shapes qkv and o_proj split K in 2 ranges, down_proj in 4
-    assert _lib.query("iron_gemm_splitk_choose", 64, 1536, 1024) == 2
-    assert _lib.query("iron_gemm_splitk_choose", 64, 1024, 2048) == 4
+    # at these shapes qkv and o_proj split K in 2 ranges, down_proj in 4 (both policies)
+    for q in ("iron_gemm_splitk_choose", "iron_gemm_i4g32_splitk_choose"):
+        assert _lib.query(q, 64, 1536, 1024) == 2
+        assert _lib.query(q, 64, 1024, 1024) == 2
+        assert _lib.query(q, 64, 1024, 2048) == 4
     w = random_weights(cfg, gpu, seed=4)
     fused = LlamaHIP(cfg, w, device=gpu)
     plain = LlamaHIP(dataclasses.replace(cfg, prefill_fuse_merge=False), w, device=gpu)
