@@ -755,18 +755,28 @@ static void launch_tile_i4(const GemmArgs& a, hipStream_t s) {
   IRON_LAUNCH(gemm_i4_kernel<T>, dim3(static_cast<unsigned>(tile_count<T>(a))), dim3(T::kThreads), 0, s, a);
 }
 
+// Shapes whose 128x128 tiles leave CUs idle (with no K split): the smaller
+// tile whose count comes closest to one per CU without going over (64 = 64x64,
+// 128 = 128x64, 0 = neither fits: the cost model's tiles). 512 tokens, cold
+// weights: 512x2048 -> 2048 19.7 -> 12.3 us (64x64), -> 3072 20.0 -> 15.9 us
+// (128x64), 512x8192 -> 2048 65.6 -> 40.5 us (64x64).
+static int small_tile(int M, int N) {
+  auto tiles = [&](int bm, int bn) { return static_cast<long long>((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (tiles(128, 128) >= 256) return 0;
+  if (tiles(64, 64) <= 256) return 64;
+  if (tiles(128, 64) <= 256) return 128;
+  return 0;
+}
+
 static void gemm_launch(const GemmArgs& a, hipStream_t s) {
-  // Shapes whose 128x128 tiles leave CUs idle (with no workspace for a K
-  // split): the smaller tile whose count comes closest to one per CU without
-  // going over. 512 tokens, cold weights: 512x2048 -> 2048 19.7 -> 12.3 us
-  // (64x64), -> 3072 20.0 -> 15.9 us (128x64), 512x8192 -> 2048 65.6 -> 40.5 us
-  // (64x64). The SwiGLU pair needs 128-column tiles.
-  if (a.splits == 1 && a.epi != kEpiSwigluPair && tile_count<TileS>(a) < 256) {
-    if (tile_count<Tile64>(a) <= 256) {
+  // The SwiGLU pair needs 128-column tiles.
+  if (a.splits == 1 && a.epi != kEpiSwigluPair) {
+    const int st = small_tile(a.M, a.N);
+    if (st == 64) {
       launch_tile<Tile64>(a, s);
       return;
     }
-    if (tile_count<Tile128x64>(a) <= 256) {
+    if (st == 128) {
       launch_tile<Tile128x64>(a, s);
       return;
     }
@@ -818,15 +828,12 @@ static int splitk_short(int M, int N, int K) {
   return s;
 }
 
-// Workgroups of the plain bf16 GEMM (gemm_launch's choice for grids that
-// 128x128 tiles leave idle: 64x64 or 128x64 tiles, at most one per CU).
+// Workgroups of the plain bf16 GEMM on a grid that 128x128 tiles leave idle
+// (gemm_launch's small_tile), or the 128x128 tile count.
 static long long plain_small_grid(int M, int N) {
-  auto tiles = [&](int bm, int bn) { return static_cast<long long>((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (tiles(128, 128) < 256) {
-    if (tiles(64, 64) <= 256) return tiles(64, 64);
-    if (tiles(128, 64) <= 256) return tiles(128, 64);
-  }
-  return tiles(128, 128);
+  const int st = small_tile(M, N);
+  const int bm = st == 0 ? 128 : st, bn = st == 0 ? 128 : 64;
+  return static_cast<long long>((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
 // bf16: a K of fewer than 64 steps is split only when the plain kernel's
