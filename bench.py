@@ -2,11 +2,12 @@
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--mode full|gemv|gemv_bf16|model|prefill|gemm_large|gemm_512|attention|floor|mfma]
+                    [--mode full|gemv|gemv_bf16|sustained|model|prefill|gemm_large|gemm_512|attention|floor|mfma]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
-runs only the Llama configuration; --mode prefill only the config 5 prefill
+runs only the Llama configuration; --mode sustained the two GEMV kernels over
+tall matrices (the streaming rate without the per-launch cost); --mode prefill only the config 5 prefill
 GEMM and the 3968-token causal attention; --mode gemm_large the 3968-token
 prefill projections and 4096^3 beside hipBLASLt; --mode gemm_512 the plain
 (no K split) 512-token projections beside hipBLASLt; --mode attention the GQA decode
@@ -316,6 +317,71 @@ def bench_gemv_bf16(torch, lib, tm, dev, n, cpu_s=0.0):
     out = _gpu_line("gemv_bf16_cfg1", kern, nbytes=nbytes, cpu=cpu)
     out["python_launch_us"] = round(b2b, 3)
     out["weight_copies"] = copies
+    return out
+
+
+def bench_gemv_sustained(torch, lib, tm, dev, cpu_s=0.0):
+    """The two GEMV kernels over tall matrices (K 2048, random codes / weights,
+    one launch per call, rotated copies): the rate once the fixed per-launch
+    cost (~2 us, profiles/floors_launch_read_mfma.md) is small beside the bytes,
+    and the incremental rate between the two sizes, (bytes2 - bytes1) /
+    (t2 - t1), which cancels it. The north_star's "sustain >= 75% of HBM
+    peak" read as streaming over many rows, beside the batch-1 configs."""
+    from iron_amd import _lib
+    from oracle import configs, ops
+
+    K = 2048
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(K, device=dev, generator=g).to(torch.bfloat16)
+    out = {}
+    for fmt, sizes in (("int4_g32", (131072, 262144)), ("bf16", (65536, 131072))):
+        pts = []
+        for M in sizes:
+            if fmt == "int4_g32":
+                nbytes = M * K // 2 + M * (K // 32) * 2 + 2 * K + 2 * M
+                copies = copies_for(nbytes)
+                ws = [(torch.randint(0, 256, (M, K // 2), dtype=torch.uint8, device=dev, generator=g),
+                       (torch.rand(M, K // 32, device=dev, generator=g) * 0.009 + 0.001).to(torch.bfloat16))
+                      for _ in range(copies)]
+            else:
+                nbytes = 2 * M * K + 2 * K + 2 * M
+                copies = copies_for(nbytes)
+                ws = [(torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16), None) for _ in range(copies)]
+            y = torch.empty(M, dtype=torch.bfloat16, device=dev)
+
+            def launch(i, s, ws=ws, y=y, M=M):
+                w, sc = ws[i % len(ws)]
+                if sc is not None:
+                    _check(lib, lib.iron_gemv_i4g32(w.data_ptr(), sc.data_ptr(), x.data_ptr(), y.data_ptr(), M, K, 1, s))
+                else:
+                    _check(lib, lib.iron_gemv_bf16(w.data_ptr(), x.data_ptr(), y.data_ptr(), M, K, 1, 0, s))
+
+            stream = _lib.stream_handle(dev)
+            for i in range(copies):
+                launch(i, stream)
+            kern = tm.rotating_us(launch, copies, 4 * copies)
+            pts.append((M, nbytes, kern, copies))
+            del ws, y
+            torch.cuda.empty_cache()
+        line = {f"M{M}": {"kernel_us": round(t, 3), "algorithmic_bytes": b, "GB/s": round(b / t / 1e3, 1),
+                          "frac_hbm": round(b / t / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": c}
+                for M, b, t, c in pts}
+        (_, b1, t1, _), (_, b2, t2, _) = pts
+        inc = (b2 - b1) / (t2 - t1) / 1e3
+        line["incremental_GB/s"] = round(inc, 1)
+        line["incremental_frac_hbm"] = round(inc / HBM_PEAK_GBS, 4)
+        out[fmt] = line
+    # CPU baseline: the same oracle GEMVs at the configs' sizes (their host rate does not depend on M)
+    if cpu_s > 0:
+        W1, x1 = configs.cfg1_gemv_bf16(M=2048, K=8192)
+        codes, scales, x2 = configs.cfg2_gemv_int4()
+        out["bf16"]["cpu_baseline"] = _cpu_line(
+            torch, lambda: ops.gemv_reference(W1, x1), cpu_s, (2 * W1.numel() + 2 * 8192 + 2 * 2048) / 1e9, "GB/s",
+            "config-1 bf16 GEMV via oracle.ops.gemv_reference (torch CPU, fp32 matvec)")
+        nb2 = codes.numel() + 2 * scales.numel() + 2 * x2.numel() + 2 * codes.shape[0]
+        out["int4_g32"]["cpu_baseline"] = _cpu_line(
+            torch, lambda: ops.gemv_int4_reference(codes, scales, x2), cpu_s, nb2 / 1e9, "GB/s",
+            "config-2 int4 GEMV via oracle.ops.gemv_int4_reference (torch CPU: dequantise, fp32 matvec)")
     return out
 
 
@@ -795,8 +861,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
-    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "model", "prefill", "gemm_large", "gemm_512", "attention", "floor",
-                                       "mfma"],
+    ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "sustained", "model", "prefill", "gemm_large", "gemm_512",
+                                       "attention", "floor", "mfma"],
                     default="full")
     args = ap.parse_args()
 
@@ -850,6 +916,8 @@ def main() -> int:
         })
     if args.mode == "gemv_bf16":
         return emit("gemv_bf16", {"gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300)})
+    if args.mode == "sustained":
+        return emit("sustained", {"gemv_sustained": bench_gemv_sustained(torch, lib, tm, dev)})
     if args.mode == "floor":
         return emit("floor", {"floor": bench_floor(torch, lib, tm, dev)})
     if args.mode == "mfma":
@@ -923,6 +991,7 @@ def main() -> int:
         cs = 0.0 if args.no_cpu_baseline else args.cpu_seconds / 3
         extra = {
             "gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300, cpu_s=cs),
+            "gemv_sustained": bench_gemv_sustained(torch, lib, tm, dev, cpu_s=cs / 2),
             "gqa_decode_cfg3": bench_gqa(torch, lib, tm, dev, 300, cpu_s=cs),
             "gqa_decode_kv4096": bench_gqa(torch, lib, tm, dev, 300, L=4096, max_len=4608, cpu_s=cs),
             "swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200, cpu_s=cs),
