@@ -390,6 +390,10 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
     XGroup xg[GPL];
 #pragma unroll
     for (int j = 0; j < GPL; ++j) build_xgroup(xr[j], xg[j]);
+    // x is prepared while the weights are still in flight: without this fence
+    // the compiler hoisted the scale conversions above it, and its wait for
+    // them (counts are in issue order) also waited for every code load.
+    __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {

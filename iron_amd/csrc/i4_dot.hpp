@@ -12,14 +12,16 @@
 
 namespace iron {
 
+// Sum of squares of the 8 bf16 of a 16-byte chunk added to acc: one v_dot2
+// per pair (a pair times itself), so no unpacking.
 __device__ __forceinline__ float sumsq_chunk(uint4 v, float acc) {
-  float a;
-  a = lo_bf16(v.x); acc = fmaf(a, a, acc); a = hi_bf16(v.x); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.y); acc = fmaf(a, a, acc); a = hi_bf16(v.y); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.z); acc = fmaf(a, a, acc); a = hi_bf16(v.z); acc = fmaf(a, a, acc);
-  a = lo_bf16(v.w); acc = fmaf(a, a, acc); a = hi_bf16(v.w); acc = fmaf(a, a, acc);
-  return acc;
+  acc = dot2_bf16(v.x, v.x, acc);
+  acc = dot2_bf16(v.y, v.y, acc);
+  acc = dot2_bf16(v.z, v.z, acc);
+  return dot2_bf16(v.w, v.w, acc);
 }
+
+constexpr uint32_t kBf16OnePair = 0x3f803f80u;  // (1.0, 1.0) as two bf16
 
 // x chunk of one group (32 bf16) rearranged into the nibble-pair order:
 // word q of the codes holds elements 8q..8q+7; the pair extracted at shift 4j
@@ -29,17 +31,22 @@ struct XGroup {
   float sum;
 };
 
+// The group's x sum takes one v_dot2 with (1, 1) per pair.
 __device__ __forceinline__ void build_xgroup(const uint4 (&xc)[4], XGroup& g) {
   float s = 0.f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const uint32_t w0 = xc[q].x, w1 = xc[q].y, w2 = xc[q].z, w3 = xc[q].w;  // (x0,x1) (x2,x3) (x4,x5) (x6,x7)
-    g.p[q * 4 + 0] = (w0 & 0xffffu) | (w2 << 16);      // (x0, x4)
-    g.p[q * 4 + 1] = (w0 >> 16) | (w2 & 0xffff0000u);  // (x1, x5)
-    g.p[q * 4 + 2] = (w1 & 0xffffu) | (w3 << 16);      // (x2, x6)
-    g.p[q * 4 + 3] = (w1 >> 16) | (w3 & 0xffff0000u);  // (x3, x7)
-    s += lo_bf16(w0) + hi_bf16(w0) + lo_bf16(w1) + hi_bf16(w1) + lo_bf16(w2) + hi_bf16(w2) + lo_bf16(w3) +
-         hi_bf16(w3);
+    // v_perm_b32 byte selects over {hi: first operand, lo: second}: 0-3 the
+    // second operand's bytes, 4-7 the first's
+    g.p[q * 4 + 0] = __builtin_amdgcn_perm(w2, w0, 0x05040100u);  // (x0, x4)
+    g.p[q * 4 + 1] = __builtin_amdgcn_perm(w2, w0, 0x07060302u);  // (x1, x5)
+    g.p[q * 4 + 2] = __builtin_amdgcn_perm(w3, w1, 0x05040100u);  // (x2, x6)
+    g.p[q * 4 + 3] = __builtin_amdgcn_perm(w3, w1, 0x07060302u);  // (x3, x7)
+    s = dot2_bf16(w0, kBf16OnePair, s);
+    s = dot2_bf16(w1, kBf16OnePair, s);
+    s = dot2_bf16(w2, kBf16OnePair, s);
+    s = dot2_bf16(w3, kBf16OnePair, s);
   }
   g.sum = s;
 }
