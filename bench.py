@@ -2,7 +2,7 @@
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--mode full|gemv|gemv_bf16|sustained|model|prefill|gemm_large|gemm_512|attention|floor|mfma]
+                    [--mode full|gemv|gemv_bf16|sustained|model|prefill|gemm_large|gemm_512|attention|floor|mfma|swiglu]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
@@ -13,7 +13,8 @@ prefill projections and 4096^3 beside hipBLASLt; --mode gemm_512 the plain
 (no K split) 512-token projections beside hipBLASLt; --mode attention the GQA decode
 attention at config 3 and at KV 4096; --mode floor the per-launch floors (an
 empty kernel as a graph node, a pure streaming read of the decode kernels'
-sizes). The modes exist for kernel traces and counters.
+sizes); --mode swiglu config 4's block (bf16, int4 in two launches, int4 in one
+launch). The modes exist for kernel traces and counters.
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
@@ -497,6 +498,24 @@ def bench_swiglu(torch, lib, tm, dev, n, cpu_s=0.0):
         cpu = _cpu_line(torch, cpu_block4, cpu_s, nbytes / 1e9, "GB/s",
                         "config-4 int4-g32 SwiGLU block (oracle.ops.dequant_planar, then swiglu_block_reference)")
     res["int4_g32"] = _gpu_line("swiglu_block_int4_cfg4", t, nbytes=nbytes, cpu=cpu)
+    # the same block as one launch (iron_swiglu_decode_i4g32: h handed over inside the launch)
+    ws = torch.zeros(int(_lib.query("iron_swiglu_decode_i4g32_workspace_bytes", E, F)), dtype=torch.uint8,
+                     device=dev)
+
+    def block1(i, s):
+        a = Q[i % reps]
+        _check(lib, lib.iron_swiglu_decode_i4g32(a["g"][0].data_ptr(), a["g"][1].data_ptr(), a["u"][0].data_ptr(),
+                                                 a["u"][1].data_ptr(), a["d"][0].data_ptr(), a["d"][1].data_ptr(),
+                                                 xd.data_ptr(), y.data_ptr(), E, F, 1, 1, nwd.data_ptr(), 1e-5,
+                                                 xd.data_ptr(), ws.data_ptr(), 100000, s))
+
+    for i in range(10):
+        block1(i, stream)
+    t1 = tm.rotating_us(block1, reps, n)
+    torch.cuda.synchronize()
+    if int(ws[:4].view(torch.int32).item()) != 0:
+        raise RuntimeError("iron_swiglu_decode_i4g32: a wait gave up during the benchmark")
+    res["int4_g32_one_launch"] = _gpu_line("swiglu_block_int4_cfg4_one_launch", t1, nbytes=nbytes, cpu=cpu)
     return res
 
 
@@ -862,7 +881,7 @@ def main() -> int:
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
     ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "sustained", "model", "prefill", "gemm_large", "gemm_512",
-                                       "attention", "floor", "mfma"],
+                                       "attention", "floor", "mfma", "swiglu"],
                     default="full")
     args = ap.parse_args()
 
@@ -918,6 +937,8 @@ def main() -> int:
         return emit("gemv_bf16", {"gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300)})
     if args.mode == "sustained":
         return emit("sustained", {"gemv_sustained": bench_gemv_sustained(torch, lib, tm, dev)})
+    if args.mode == "swiglu":
+        return emit("swiglu", {"swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200)})
     if args.mode == "floor":
         return emit("floor", {"floor": bench_floor(torch, lib, tm, dev)})
     if args.mode == "mfma":

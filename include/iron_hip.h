@@ -97,6 +97,34 @@ int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x, void* y, 
 int iron_gemv_i4g32(const void* codes, const void* scales, const void* x, void* y, int M, int K, int is_signed,
                     void* stream);
 
+/* Bytes of the workspace of iron_swiglu_decode_i4g32 for hidden E and FFN F
+ * (-1 for shapes it does not take). */
+long long iron_swiglu_decode_i4g32_workspace_bytes(int E, int F);
+
+/* The decode SwiGLU block in ONE launch, int4 group-32 weights, E = 2048,
+ * F = 8192:
+ *   h = bf16(silu(Wg xn) * (Wu xn)),  y = bf16(Wd h + residual)
+ * with xn as in iron_gemv_i4g32_fused's norm_mode (0 none, 1 RMSNorm with
+ * norm_w, 2 outputs scaled by rsqrt(mean(x^2) + eps), norm weight folded into
+ * Wg/Wu). Codes (rows, K/2) and scales (rows, K/32) as iron_gemv_i4g32;
+ * residual may be NULL, and x, residual and y may alias. y is bit-identical
+ * to iron_gemv_i4g32_fused(gate, up, x -> h) then iron_gemv_i4g32_fused(down,
+ * h -> y, residual). The 256 workgroups run at once (refused with IRON_EINVAL
+ * when the device cannot hold them) and hand h over inside the launch through
+ * `workspace` (iron_swiglu_decode_i4g32_workspace_bytes, 256-byte aligned,
+ * zero-filled once; its contents carry over between calls, so calls on one
+ * workspace must not overlap). Waits are bounded by wait_us microseconds: on
+ * timeout, or when the workspace's first 32-bit word (status) is already
+ * nonzero, the call ends without writing y and leaves the status word nonzero;
+ * zero-fill the workspace before calling again. Replaces the SwiGLUDecode
+ * runlist iron/operators/swiglu_decode/op.py:56-62 (GEMV gate, GEMV up, SiLU,
+ * ElementwiseMul, GEMV down) and the MLP half of the decode layer
+ * iron/applications/llama_3.2_1b/llama_npu.py:534-550 (RMSNorm through the residual add). */
+int iron_swiglu_decode_i4g32(const void* gate_codes, const void* gate_scales, const void* up_codes,
+                             const void* up_scales, const void* down_codes, const void* down_scales, const void* x,
+                             void* y, int E, int F, int is_signed, int norm_mode, const void* norm_w, float eps,
+                             const void* residual, void* workspace, unsigned wait_us, void* stream);
+
 /* int4 counterpart of iron_gemv_bf16_fused (codes2/scales2 = SwiGLU up). */
 int iron_gemv_i4g32_fused(const void* codes, const void* scales, const void* codes2, const void* scales2,
                           const void* x, void* y, int M, int K, int is_signed, int norm_mode, const void* norm_w,

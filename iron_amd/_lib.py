@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
     "iron_llama_decode_fused": [_P, _I, _P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _I, _F, _F, _P, _P, _P, _P, _P,
                                 ctypes.c_uint, _I, _P],
     "iron_llama_decode_head": [_P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P],
+    "iron_swiglu_decode_i4g32": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _F, _P, _P, ctypes.c_uint, _P],
     "iron_probe_empty": [_I, _P],
     "iron_probe_read": [_P, _LL, _P, _LL, _I, _P],
     "iron_probe_mfma": [_I, _I, _I, _I, _P, _P, _LL, _P],
@@ -74,6 +75,7 @@ QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_chunk_positions": (_I, [_I, _I, _I, _I, _I, _P]),
     "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
     "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
+    "iron_swiglu_decode_i4g32_workspace_bytes": (_LL, [_I, _I]),
     "iron_xcd_round_robin": (_I, [_P]),
     "iron_gemm_splitk_choose": (_I, [_I, _I, _I]),
     "iron_gemm_i4g32_splitk_choose": (_I, [_I, _I, _I]),

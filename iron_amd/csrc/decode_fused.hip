@@ -40,6 +40,7 @@
 #include "iron_common.hpp"
 #include "i4_dot.hpp"
 #include "decode_attn.hpp"
+#include "exchange.hpp"
 #include "../../include/iron_hip.h"
 
 namespace iron {
@@ -102,27 +103,6 @@ struct FusedArgs {
   unsigned wait_ticks;  // 100 MHz ticks
 };
 
-typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2_v __attribute__((ext_vector_type(2)));
-constexpr int kSc1 = 16;  // cache-policy bits of the buffer builtins: sc1 (agent scope)
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t xch_rsrc(const unsigned char* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(base), 0, 0x7fffffff, kBufferFlags);
-}
-// pairs p and p + 1 (p even)
-__device__ __forceinline__ u32x4_v ld_pairs2(__amdgpu_buffer_rsrc_t r, int p) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, p * 8, 0, kSc1);
-}
-__device__ __forceinline__ u32x2_v ld_pair(__amdgpu_buffer_rsrc_t r, int p) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, p * 8, 0, kSc1);
-}
-__device__ __forceinline__ void st_pairs2(__amdgpu_buffer_rsrc_t r, int p, uint32_t d0, uint32_t d1, unsigned tag) {
-  __builtin_amdgcn_raw_buffer_store_b128(u32x4_v{d0, tag, d1, tag}, r, p * 8, 0, kSc1);
-}
-__device__ __forceinline__ void st_pair(__amdgpu_buffer_rsrc_t r, int p, uint32_t d, unsigned tag) {
-  __builtin_amdgcn_raw_buffer_store_b64(u32x2_v{d, tag}, r, p * 8, 0, kSc1);
-}
-
 // threadIdx.x as a value the compiler must treat as new at every call: the
 // persistent loop then recomputes each thread-dependent address where it is
 // used instead of hoisting dozens of them out of the loop and keeping them
@@ -133,13 +113,6 @@ __device__ __forceinline__ int opaque_tid() {
   return t;
 }
 
-__device__ __forceinline__ unsigned long long now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
-__device__ __forceinline__ unsigned read_status(const unsigned* status) {
-  return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void give_up(unsigned* status, unsigned bit) {
-  __hip_atomic_fetch_or(status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // Workgroup barrier for LDS only: the weight and cache loads in flight are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 

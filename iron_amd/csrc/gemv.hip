@@ -47,16 +47,6 @@ struct GemvArgs {
   unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
 };
 
-// Normalises the 8 bf16 values of an x chunk: bf16(x * inv * w).
-__device__ __forceinline__ uint4 normalize_chunk(uint4 xv, uint4 wv, float inv) {
-  uint4 r;
-  r.x = pack_bf16x2(lo_bf16(xv.x) * inv * lo_bf16(wv.x), hi_bf16(xv.x) * inv * hi_bf16(wv.x));
-  r.y = pack_bf16x2(lo_bf16(xv.y) * inv * lo_bf16(wv.y), hi_bf16(xv.y) * inv * hi_bf16(wv.y));
-  r.z = pack_bf16x2(lo_bf16(xv.z) * inv * lo_bf16(wv.z), hi_bf16(xv.z) * inv * hi_bf16(wv.z));
-  r.w = pack_bf16x2(lo_bf16(xv.w) * inv * lo_bf16(wv.w), hi_bf16(xv.w) * inv * hi_bf16(wv.w));
-  return r;
-}
-
 __device__ __forceinline__ float dot_chunk(uint4 w, uint4 x, float acc) {
   acc = dot2_bf16(w.x, x.x, acc);
   acc = dot2_bf16(w.y, x.y, acc);
@@ -106,15 +96,6 @@ __device__ __forceinline__ void publish_key(unsigned long long* keys, size_t key
     const size_t idx = key_idx * R + g;
     if (idx < n_keys) keys[idx] = b;
   }
-}
-
-// Workgroup index -> logical tile. With `enable` (and a grid that is a
-// multiple of 8), each XCD (workgroup b runs on XCD b % 8) owns one
-// contiguous eighth of the rows: its weight rows are adjacent in HBM and every
-// 64-byte line of y is written from one L2 only.
-__device__ __forceinline__ int xcd_block(int enable) {
-  const int nb = gridDim.x, b = blockIdx.x;
-  return (!enable || (nb & 7)) ? b : (b & 7) * (nb >> 3) + (b >> 3);
 }
 
 // The epoch word of the one-launch decode step (its exchange tags) moves on

@@ -176,6 +176,25 @@ __device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
   return __builtin_amdgcn_rsqf(ss / static_cast<float>(n) + eps);
 }
 
+// Normalises the 8 bf16 values of an x chunk: bf16(x * inv * w).
+__device__ __forceinline__ uint4 normalize_chunk(uint4 xv, uint4 wv, float inv) {
+  uint4 r;
+  r.x = pack_bf16x2(lo_bf16(xv.x) * inv * lo_bf16(wv.x), hi_bf16(xv.x) * inv * hi_bf16(wv.x));
+  r.y = pack_bf16x2(lo_bf16(xv.y) * inv * lo_bf16(wv.y), hi_bf16(xv.y) * inv * hi_bf16(wv.y));
+  r.z = pack_bf16x2(lo_bf16(xv.z) * inv * lo_bf16(wv.z), hi_bf16(xv.z) * inv * hi_bf16(wv.z));
+  r.w = pack_bf16x2(lo_bf16(xv.w) * inv * lo_bf16(wv.w), hi_bf16(xv.w) * inv * hi_bf16(wv.w));
+  return r;
+}
+
+// Workgroup index -> logical tile. With `enable` (and a grid that is a
+// multiple of 8), each XCD (workgroup b runs on XCD b % 8) owns one
+// contiguous eighth of the rows: its weight rows are adjacent in HBM and every
+// 64-byte line of y is written from one L2 only.
+__device__ __forceinline__ int xcd_block(int enable) {
+  const int nb = gridDim.x, b = blockIdx.x;
+  return (!enable || (nb & 7)) ? b : (b & 7) * (nb >> 3) + (b >> 3);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float gelu_tanh_f32(float x) {

@@ -131,3 +131,32 @@ def test_gqa_decode_ex_rejects_unknown_flags_on_host():
 
     with pytest.raises(_lib.IronHipError, match="unknown flags"):
         _lib.call("iron_gqa_decode_ex", 16, 16, 16, 16, 16, 16, 128, 16, 256, 32, 8, 64, 128, 0, None, 0.125, 4, None)
+
+
+def test_swiglu_decode_one_launch_rejects_on_host():
+    """The one-launch SwiGLU block takes E=2048, F=8192 only, checks its
+    pointers, alignments, norm mode and wait bound before anything runs."""
+    from iron_amd import _lib
+
+    assert _lib.query("iron_swiglu_decode_i4g32_workspace_bytes", 2048, 8192) == 256 + 8 * 4096
+    assert _lib.query("iron_swiglu_decode_i4g32_workspace_bytes", 4096, 8192) == -1
+    p = 1 << 20  # a 256-byte-aligned stand-in address: nothing is launched
+
+    def call(E=2048, F=8192, mode=2, norm_w=None, ws=p, wait=1000, x=p):
+        _lib.call("iron_swiglu_decode_i4g32", p, p, p, p, p, p, x, p, E, F, 1, mode, norm_w, 1e-5, None, ws, wait,
+                  None)
+
+    with pytest.raises(_lib.IronHipError, match="E=4096"):
+        call(E=4096)
+    with pytest.raises(_lib.IronHipError, match="norm_mode=3"):
+        call(mode=3)
+    with pytest.raises(_lib.IronHipError, match="needs norm_w"):
+        call(mode=1)
+    with pytest.raises(_lib.IronHipError, match="wait_us=0"):
+        call(wait=0)
+    with pytest.raises(_lib.IronHipError, match="aligned"):
+        call(ws=p + 16)
+    with pytest.raises(_lib.IronHipError, match="aligned"):
+        call(x=p + 2)
+    with pytest.raises(_lib.IronHipError, match="null pointer"):
+        call(ws=None)
