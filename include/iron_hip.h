@@ -226,8 +226,13 @@ long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_
  * device; -1 if the shape is invalid. The shape of a launch depends on the
  * position, so a caller that captures decode steps into graphs with a device
  * position captures one graph per shape and replays the one this returns for
- * the position at hand. No reference counterpart: it describes a launch. */
+ * the position at hand. No reference counterpart: it describes a launch.
+ * This form answers for calls without IRON_GQA_KV_RESIDENT; the _ex form takes
+ * the flags word of iron_gqa_decode_ex (the switch to 128-position chunks
+ * comes earlier for resident caches). */
 int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, void* stream);
+int iron_gqa_decode_chunk_positions_ex(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos, int flags,
+                                       void* stream);
 
 /* One GQA decode step (head_dim 64, group n_heads/n_kv_heads in {1,2,4,8}).
  * With n_kv_heads a multiple of 8, on a device whose workgroups with ids
@@ -235,7 +240,8 @@ int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, i
  * launch after a one-wave counter reset (each KV head's chunks run on one
  * XCD, and the last of them to finish merges them there; chunks of 64
  * positions, or of 128 once the active 128-position chunks of all KV heads
- * reach half the device's CUs: iron_gqa_decode_chunk_positions); otherwise
+ * reach the device's CU count, or half of it with IRON_GQA_KV_RESIDENT:
+ * iron_gqa_decode_chunk_positions_ex); otherwise
  * 64-position chunk partials, then a merge kernel:
  *   q' = rope(q, pos), k' = rope(k_new, pos)   (two halves; angles fp32
  *                                               (angle_rows, 64) [cos,sin])

@@ -73,6 +73,7 @@ SIGNATURES: dict[str, list] = {
 QUERIES: dict[str, tuple] = {
     "iron_gqa_decode_workspace_bytes": (_LL, [_I, _I, _I, _I]),
     "iron_gqa_decode_chunk_positions": (_I, [_I, _I, _I, _I, _I, _P]),
+    "iron_gqa_decode_chunk_positions_ex": (_I, [_I, _I, _I, _I, _I, _I, _P]),
     "iron_gqa_decode_noalloc_max_bytes": (_LL, []),
     "iron_llama_decode_fused_exchange_bytes": (_LL, [_I]),
     "iron_swiglu_decode_i4g32_workspace_bytes": (_LL, [_I, _I]),

@@ -378,8 +378,8 @@ class LlamaHIP:
         cfg = self.cfg
         if self.fused:
             return 64
-        return int(_lib.query("iron_gqa_decode_chunk_positions", cfg.n_heads, cfg.n_kv_groups, cfg.head_dim,
-                              cfg.max_seq_len, pos, self._stream()))
+        return int(_lib.query("iron_gqa_decode_chunk_positions_ex", cfg.n_heads, cfg.n_kv_groups, cfg.head_dim,
+                              cfg.max_seq_len, pos, self.kv_flags, self._stream()))
 
     def _decode_shapes(self) -> dict:
         """One position hint per attention launch shape the decode can take

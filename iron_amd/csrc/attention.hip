@@ -402,15 +402,23 @@ static long long decode_head_stride(int G, int max_len) {
   return (static_cast<long long>(decode_nsplit(max_len)) * decode_part_stride(G) + 63) / 64 * 64;
 }
 
-static bool decode_long_chunks(int n_kv_heads, int max_len, int pos);
+static bool decode_long_chunks(int n_kv_heads, int max_len, int pos, bool resident);
 
-extern "C" int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos,
-                                               void* stream) {
+extern "C" int iron_gqa_decode_chunk_positions_ex(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos,
+                                                  int flags, void* stream) {
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads || head_dim != kD || max_len <= 0) return -1;
+  if (flags & ~(IRON_GQA_KV_RESIDENT | IRON_GQA_COUNTERS_ZERO)) return -1;
   const int G = n_heads / n_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
   const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(static_cast<hipStream_t>(stream)) == 1;
-  return one && decode_long_chunks(n_kv_heads, max_len, pos) ? 16 * kDecWaves1 : kDecChunk;
+  return one && decode_long_chunks(n_kv_heads, max_len, pos, (flags & IRON_GQA_KV_RESIDENT) != 0)
+             ? 16 * kDecWaves1
+             : kDecChunk;
+}
+
+extern "C" int iron_gqa_decode_chunk_positions(int n_heads, int n_kv_heads, int head_dim, int max_len, int pos,
+                                               void* stream) {
+  return iron_gqa_decode_chunk_positions_ex(n_heads, n_kv_heads, head_dim, max_len, pos, 0, stream);
 }
 
 extern "C" long long iron_gqa_decode_workspace_bytes(int n_heads, int n_kv_heads, int head_dim, int max_len) {
@@ -442,14 +450,19 @@ static int device_cus() {
 
 // Whether the one-launch path takes 128-position chunks (kDecWaves1 waves) for
 // a call at position `pos` (the position, or with a device position the
-// caller's hint of it; -1: no hint, the cache's last slot): when the active
-// 128-position chunks of all KV heads reach half the CUs. Below that, more
-// and smaller chunks keep more CUs loading; above it, half the partials to
-// merge and half the waves to dispatch win (decode at KV 512 and 4096 in the
-// model measured each way). Any choice gives a correct result.
-static bool decode_long_chunks(int n_kv_heads, int max_len, int pos) {
+// caller's hint of it; -1: no hint, the cache's last slot). Below the switch,
+// more and smaller chunks keep more CUs loading; above it, half the partials
+// to merge and half the waves to dispatch win. With resident caches
+// (IRON_GQA_KV_RESIDENT: K/V served from the Infinity Cache) the switch is
+// where the active 128-position chunks of all KV heads reach half the CUs
+// (decode in the model measured each way at KV 512 to 3968); with caches
+// streamed from HBM it is where those chunks alone reach the CU count (8 KV
+// heads: KV 2048 5.07 us with 64-position chunks against 5.31 with 128, KV
+// 4096 6.20 against 5.89). Any choice gives a correct result.
+static bool decode_long_chunks(int n_kv_heads, int max_len, int pos, bool resident) {
   const int p = pos < 0 || pos >= max_len ? max_len - 1 : pos;
-  return static_cast<long long>(p / (16 * kDecWaves1) + 1) * n_kv_heads * 2 >= device_cus();
+  const long long active = static_cast<long long>(p / (16 * kDecWaves1) + 1) * n_kv_heads;
+  return (resident ? 2 * active : active) >= device_cus();
 }
 
 template <int G, bool RES>
@@ -510,7 +523,7 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(s) == 1;
-  const bool long_chunks = one && decode_long_chunks(n_kv_heads, max_len, pos);
+  const bool long_chunks = one && decode_long_chunks(n_kv_heads, max_len, pos, (flags & IRON_GQA_KV_RESIDENT) != 0);
   if (one && !(flags & IRON_GQA_COUNTERS_ZERO))
     IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
   if (flags & IRON_GQA_KV_RESIDENT) {

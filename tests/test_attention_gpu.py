@@ -141,13 +141,18 @@ def test_gqa_decode_position_hint_picks_the_shape(gpu):
     """With a device position, the host position is a hint that picks the
     launch shape (64- or 128-position chunks) and nothing else: both shapes
     match the oracle at the same device position, and the shape query reports
-    what each hint picks (64 below half the CUs' worth of 128-position chunks,
-    128 above)."""
+    what each hint picks (64 below the CUs' worth of 128-position chunks, or
+    half of it for resident caches; 128 above)."""
     from iron_amd import _lib
     max_len = 4224
     s = _lib.stream_handle(gpu)
     shape = lambda p: _lib.query("iron_gqa_decode_chunk_positions", 32, 8, 64, max_len, p, s)
+    shape_ex = lambda p, f: _lib.query("iron_gqa_decode_chunk_positions_ex", 32, 8, 64, max_len, p, f, s)
     assert shape(0) == 64 and shape(max_len - 1) == 128 and shape(-1) == 128
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    mid = 128 * (cus // 8 - 1) - 1  # last position whose 128-position chunks (8 KV heads) stay below the CU count
+    assert shape(mid) == 64 and shape_ex(mid, 0) == 64 and shape_ex(mid, 1) == 128 and shape_ex(mid, 3) == 128
+    assert shape_ex(0, 1) == 64 and shape_ex(max_len - 1, 0) == 128 and shape_ex(0, 4) == -1
     assert _lib.query("iron_gqa_decode_chunk_positions", 8, 2, 64, max_len, max_len - 1, s) == 64  # two launches
     assert _lib.query("iron_gqa_decode_chunk_positions", 32, 2, 64, max_len, 0, s) == -1  # group of 16
     assert _lib.query("iron_gqa_decode_chunk_positions", 32, 8, 32, max_len, 0, s) == -1
