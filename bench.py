@@ -2,7 +2,7 @@
 """Benchmark of the IRON decode/prefill operator path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--mode full|gemv|gemv_bf16|sustained|model|prefill|gemm_large|gemm_512|attention|floor|mfma|swiglu]
+                    [--mode full|gemv|gemv_bf16|sustained|model|prefill|gemm_large|gemm_512|attention|floor|mfma|swiglu|trace]
 
 --mode gemv runs only the headline kernel (plus three 64 MiB device copies
 that calibrate rocprofv3's FETCH_SIZE / WRITE_SIZE counters); --mode model
@@ -14,7 +14,10 @@ prefill projections and 4096^3 beside hipBLASLt; --mode gemm_512 the plain
 attention at config 3 and at KV 4096; --mode floor the per-launch floors (an
 empty kernel as a graph node, a pure streaming read of the decode kernels'
 sizes); --mode swiglu config 4's block (bf16, int4 in two launches, int4 in one
-launch). The modes exist for kernel traces and counters.
+launch); --mode trace per-workgroup phase traces (iron_trace_next_launch) of the
+decode attention, the headline int4 GEMV and the one-launch SwiGLU block, with
+Perfetto JSON under gpurun_out/traces. The modes exist for kernel traces and
+counters.
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
@@ -519,6 +522,112 @@ def bench_swiglu(torch, lib, tm, dev, n, cpu_s=0.0):
     return res
 
 
+def _traced(torch, dev, launch, copies, calls, tag):
+    """Device phase traces (iron_trace_next_launch) of `calls` calls of
+    launch(i, stream), each on rotated (cold) inputs after a warm round: the
+    spread of their spans, and the phase summary of the median-span call,
+    whose Perfetto JSON goes to gpurun_out/traces/<tag>.json."""
+    from iron_amd import _lib
+    from iron_amd.common import tracing_utils as tu
+
+    s = _lib.stream_handle(dev)
+    buf = tu.new_buffer(1 << 16, dev)
+    for i in range(copies):
+        launch(i, s)
+    runs = []
+    for i in range(calls):
+        buf.zero_()
+        tu.arm(buf)
+        launch(i, s)
+        torch.cuda.synchronize()
+        recs = tu.parse_records(buf)
+        summ = tu.phase_summary(recs)
+        runs.append((max(v["span_ns"] for v in summ.values()), recs, summ))
+    runs.sort(key=lambda r: r[0])
+    span, recs, summ = runs[len(runs) // 2]
+    out_dir = Path("gpurun_out") / "traces"
+    out_dir.mkdir(parents=True, exist_ok=True)
+    with open(out_dir / f"{tag}.json", "w") as f:
+        json.dump(tu.perfetto_json(recs), f)
+    tu.print_cycles_summary(summ)
+    rnd = lambda v: round(v, 1) if isinstance(v, float) else v
+    return {"calls": calls, "span_ns": {"min": round(runs[0][0], 1), "median": round(span, 1),
+                                         "max": round(runs[-1][0], 1)},
+            "median_call": {k: {"workgroups": v["workgroups"], "span_ns": round(v["span_ns"], 1),
+                                "points": [{kk: rnd(vv) for kk, vv in p.items()} for p in v["points"]]}
+                            for k, v in summ.items()}}
+
+
+def bench_trace(torch, lib, dev, calls=25):
+    """--mode trace: per-workgroup phase traces of the decode attention (config
+    3 and KV 4096, streamed caches), the headline int4 GEMV (config 2) and the
+    one-launch SwiGLU block (config 4), on cold inputs."""
+    from iron_amd import _lib
+    from oracle import configs, ops
+
+    res = {}
+    H, Hkv, D = 32, 8, 64
+    for L, max_len in ((2048, 2048), (4096, 4608)):
+        q, kn, vn, kc, vc, pos, angles = configs.cfg3_gqa_decode(n_heads=H, n_kv=Hkv, head_dim=D, L=L)
+        if max_len > L:
+            pad = torch.zeros(Hkv, max_len - L, D, dtype=kc.dtype)
+            kc, vc = torch.cat([kc, pad], 1), torch.cat([vc, pad], 1)
+            angles = ops.rope_angles_table(D, max_len, theta=500000.0)
+        copies = copies_for(2 * Hkv * L * D * 2)
+        KC = [kc.to(dev) for _ in range(copies)]
+        VC = [vc.to(dev) for _ in range(copies)]
+        qd, knd, vnd, ad = q.to(dev), kn.to(dev), vn.to(dev), angles.to(dev)
+        out = torch.empty(H, D, dtype=torch.bfloat16, device=dev)
+        ws = torch.zeros(int(lib.iron_gqa_decode_workspace_bytes(H, Hkv, D, max_len)), dtype=torch.uint8, device=dev)
+
+        def attn(i, s):
+            _check(lib, lib.iron_gqa_decode_ex(qd.data_ptr(), knd.data_ptr(), vnd.data_ptr(), KC[i % copies].data_ptr(),
+                                               VC[i % copies].data_ptr(), ad.data_ptr(), angles.shape[0],
+                                               out.data_ptr(), ws.data_ptr(), H, Hkv, D, max_len, pos, None,
+                                               1.0 / math.sqrt(D), 2, s))
+
+        res["gqa_decode_cfg3" if L == 2048 else "gqa_decode_kv4096"] = _traced(
+            torch, dev, attn, copies, calls, "gqa_decode_cfg3" if L == 2048 else "gqa_decode_kv4096")
+        del KC, VC
+    codes, scales, x = configs.cfg2_gemv_int4()
+    copies = copies_for(codes.numel() + 2 * scales.numel())
+    C = [codes.to(dev) for _ in range(copies)]
+    S = [scales.to(dev) for _ in range(copies)]
+    xd = x.to(dev)
+    y = torch.empty(8192, dtype=torch.bfloat16, device=dev)
+
+    def gemv(i, s):
+        _check(lib, lib.iron_gemv_i4g32(C[i % copies].data_ptr(), S[i % copies].data_ptr(), xd.data_ptr(),
+                                        y.data_ptr(), 8192, 2048, 1, s))
+
+    res["gemv_int4_cfg2"] = _traced(torch, dev, gemv, copies, calls, "gemv_int4_cfg2")
+    del C, S
+    E, F = 2048, 8192
+    xb, nw, Wg, Wu, Wd = configs.cfg4_swiglu_block(E, F)
+    q = []
+    for W in (Wg, Wu, Wd):
+        c = torch.empty(W.shape[0], W.shape[1] // 2, dtype=torch.uint8, device=dev)
+        sc = torch.empty(W.shape[0], W.shape[1] // 32, dtype=torch.bfloat16, device=dev)
+        _check(lib, lib.iron_quantize_i4g32(W.to(dev).data_ptr(), c.data_ptr(), sc.data_ptr(), W.shape[0], W.shape[1],
+                                            _lib.stream_handle(dev)))
+        q += [c, sc]
+    copies = copies_for(sum(t.numel() * t.element_size() for t in q))
+    Q = [q] + [[t.clone() for t in q] for _ in range(copies - 1)]
+    xd, nwd = xb.to(dev), nw.to(dev)
+    yb = torch.empty(E, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(int(_lib.query("iron_swiglu_decode_i4g32_workspace_bytes", E, F)), dtype=torch.uint8, device=dev)
+
+    def swiglu(i, s):
+        a = Q[i % copies]
+        _check(lib, lib.iron_swiglu_decode_i4g32(*(t.data_ptr() for t in a), xd.data_ptr(), yb.data_ptr(), E, F, 1, 1,
+                                                 nwd.data_ptr(), 1e-5, xd.data_ptr(), ws.data_ptr(), 100000, s))
+
+    res["swiglu_one_launch_cfg4"] = _traced(torch, dev, swiglu, copies, calls, "swiglu_one_launch_cfg4")
+    if int(ws[:4].view(torch.int32).item()) != 0:
+        raise RuntimeError("iron_swiglu_decode_i4g32: a wait gave up during the trace")
+    return res
+
+
 def bench_prefill_gemm(torch, lib, tm, dev, n, int4=False, cpu_s=0.0, shape=(512, 2048, 8192)):
     """Config 5 prefill GEMM M=512 K=2048 N=8192 (bf16 weights, or int4-g32
     weights dequantised in the kernel's prologue), weights rotated through the
@@ -881,7 +990,7 @@ def main() -> int:
                     help="host-time budget of the config 2 and model-decode CPU baselines (the other configs' "
                     "baselines get a third of it each)")
     ap.add_argument("--mode", choices=["full", "gemv", "gemv_bf16", "sustained", "model", "prefill", "gemm_large", "gemm_512",
-                                       "attention", "floor", "mfma", "swiglu"],
+                                       "attention", "floor", "mfma", "swiglu", "trace"],
                     default="full")
     args = ap.parse_args()
 
@@ -937,6 +1046,8 @@ def main() -> int:
         return emit("gemv_bf16", {"gemv_bf16_cfg1": bench_gemv_bf16(torch, lib, tm, dev, 300)})
     if args.mode == "sustained":
         return emit("sustained", {"gemv_sustained": bench_gemv_sustained(torch, lib, tm, dev)})
+    if args.mode == "trace":
+        return emit("trace", {"trace": bench_trace(torch, lib, dev)})
     if args.mode == "swiglu":
         return emit("swiglu", {"swiglu_block_cfg4": bench_swiglu(torch, lib, tm, dev, 200)})
     if args.mode == "floor":

@@ -40,6 +40,25 @@ int iron_abi_version(void);
  * 216-219). Disarmed after that call; NULL, NULL disarms. Results unchanged. */
 int iron_time_next_launch(void* start_event, void* stop_event);
 
+/* Device phase trace of the calling thread's next entry-point call: the
+ * MI355X counterpart of the reference's per-design trace buffers
+ * (trace_size, iron/operators/_trace.py:17-71) that
+ * iron/common/tracing_utils.py:49-115 turns into Perfetto JSON and a cycles
+ * summary. Kernels with trace points (iron_gqa_decode and its variants,
+ * iron_gemv_i4g32 and iron_gemv_i4g32_fused on their fast path,
+ * iron_swiglu_decode_i4g32) write one 64-byte record per workgroup into
+ * `buffer` (device memory, 64-byte aligned, zero-filled by the caller), from
+ * the workgroup's first thread, at record index = the workgroup's linear id:
+ *   uint32 kernel id (1 gqa_decode, 2 gemv_i4, 3 swiglu_decode_i4),
+ *   uint32 workgroup, uint32 XCC_ID, uint32 HW_ID register,
+ *   uint64 stamps[6]: s_memrealtime (100 MHz, one clock for every XCD) when
+ *   the workgroup passed each of the kernel's trace points (0 where it did
+ *   not reach one).
+ * A call whose kernel needs more records than `bytes` holds is refused with
+ * IRON_EINVAL before it launches; calls without trace points ignore it. The
+ * trace is disarmed by that call; NULL disarms. Outputs are unchanged. */
+int iron_trace_next_launch(void* buffer, long long bytes);
+
 /* Epilogue codes shared by GEMV and GEMM. GELU_TANH is the tanh approximation
  * of iron/operators/gemv/reference.py:69-76; GELU_SIGMOID is x*sigmoid(1.702x)
  * of iron/operators/flm/gemm/reference.py:8-31. */

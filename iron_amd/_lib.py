@@ -25,6 +25,7 @@ _LL = ctypes.c_longlong
 # name -> argtypes (every function returns int, 0 = success) ...
 SIGNATURES: dict[str, list] = {
     "iron_time_next_launch": [_P, _P],
+    "iron_trace_next_launch": [_P, _LL],
     "iron_gemv_bf16": [_P, _P, _P, _I, _I, _I, _I, _P],
     "iron_gemv_bf16_fused": [_P, _P, _P, _P, _I, _I, _I, _P, _F, _P, _I, _P, _P],
     "iron_gemv_i4g32": [_P, _P, _P, _P, _I, _I, _I, _P],

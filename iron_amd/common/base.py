@@ -210,15 +210,28 @@ class HIPOperator(AIEOperatorBase):
                 raise ValueError(f"argument {i} of {type(self).__name__} must be contiguous")
 
     def get_callable(self) -> Callable[..., Any]:
+        """fn(*tensors) in get_arg_spec() order. With a positive trace size (the
+        operator's ``trace_size`` field, else ``IRON_TRACE_SIZE``) every call
+        arms a zero-filled device buffer of that many bytes for its kernels'
+        phase records (iron_trace_next_launch) and leaves it in
+        ``fn.trace_buffer`` for ``tracing_utils.dump_traces`` (the reference's
+        full-ELF callable and its trace buffer, iron/common/sequence.py:675-688)."""
         if not self._compiled:
             self.compile()
         _lib.load()
+        from .tracing_utils import arm, new_buffer, resolve_trace_size
+
+        trace_size = resolve_trace_size(getattr(self, "trace_size", None))
 
         def call(*args: torch.Tensor):
             self.validate_args(args)
+            if trace_size > 0:
+                call.trace_buffer = new_buffer(trace_size, args[0].device)
+                arm(call.trace_buffer)
             self._launch(*args, stream=_lib.stream_handle(args[0].device))
 
         call.operator = self
+        call.trace_buffer = None
         return call
 
 

@@ -521,6 +521,8 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
   a.angle_rows = angle_rows;
   a.nsplit = decode_nsplit(max_len);
   a.scale_log2 = scale * 1.4426950408889634f;
+  // at most one record per 64-position chunk of every KV head (the grid of either launch shape)
+  if (int rc = take_trace(who, static_cast<long long>(a.nsplit) * n_kv_heads, &a.trace)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool one = n_kv_heads % kXcds == 0 && xcd_round_robin(s) == 1;
   const bool long_chunks = one && decode_long_chunks(n_kv_heads, max_len, pos, (flags & IRON_GQA_KV_RESIDENT) != 0);

@@ -32,6 +32,7 @@
 #pragma once
 
 #include "iron_common.hpp"
+#include "trace.hpp"
 
 #include <type_traits>
 
@@ -60,6 +61,7 @@ struct DecodeArgs {
   int angle_rows;
   int nsplit;             // chunks per KV head
   float scale_log2;       // log2(e) * scale
+  void* trace;            // phase trace records (trace.hpp), or null
 };
 
 // One chunk's partial: G x 64 unnormalised outputs, then (maximum, sum) of
@@ -263,6 +265,10 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   __shared__ __attribute__((aligned(16))) unsigned char v_s[NW][16 * 128];  // each wave's 16 V rows
 
   const int tid = io.thread(), lane = tid & (kWave - 1), w = tid >> 6;
+  // trace points: 0 start, 1 q in LDS, 2 scores and P V done, 3 partial stored
+  // (acknowledged on the one-launch path), 4 counted in, 5 merged (last arriver)
+  const unsigned twg = blockIdx.x + blockIdx.y * gridDim.x;
+  const unsigned long long t_start = trace_clock();
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * CH;
@@ -310,6 +316,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // K/V loads are ordinary, allocating loads (decode +0.9%). Otherwise they are
   // streaming loads, faster when the caches come from HBM every time.
   const DecodeKv kv = io.template kv_rows<RES>(a, p0, j);
+  trace_write(a.trace, kTraceGqaDecode, twg, 0, t_start);
   uint4 k0 = kv.k0, k1 = kv.k1;
   unsigned char* vblk = v_s[w];
   const uint4 vraw[2] = {kv.v0, kv.v1};
@@ -330,6 +337,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // barrier without a wait for the K/V loads in flight (__syncthreads would
   // wait for all of them); the memory clobber keeps the q_s accesses on their sides
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  trace_stamp(a.trace, kTraceGqaDecode, twg, 1);
   const int hq = r & (G - 1);
   const dec_bf16x8 qb0 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + cq * 8]);
   const dec_bf16x8 qb1 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + (cq + 4) * 8]);
@@ -433,6 +441,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   else
     wave_body(std::false_type{});
   __syncthreads();
+  trace_stamp(a.trace, kTraceGqaDecode, twg, 2);
 
   // the chunk's partial: the four waves merged
   float* part = a.part + static_cast<size_t>(j) * a.head_stride + static_cast<size_t>(s) * PS;
@@ -451,11 +460,13 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     part[t] = o;
     if (t % D == 0) *reinterpret_cast<float2*>(part + G * D + 2 * g) = make_float2(M, l);
   }
+  if constexpr (!MERGE) trace_stamp(a.trace, kTraceGqaDecode, twg, 3);
   if constexpr (MERGE) {
     __shared__ int last_s;
     const int nact = (L + CH - 1) / CH;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have reached the L2
     __syncthreads();
+    trace_stamp(a.trace, kTraceGqaDecode, twg, 3);
     if (tid == 0) {  // an atomic in the XCD's L2, where the partials are
       unsigned* c = a.ctr + static_cast<size_t>(j) * kCtrStride;
       const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -464,6 +475,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
       last_s = last;
     }
     __syncthreads();
+    trace_stamp(a.trace, kTraceGqaDecode, twg, 4);
     if (!last_s) return;
     // An Io whose persistent workgroups merge again later (Io::kStaleL1) may
     // hold lines of an earlier merge's partials in this CU's L1: an
@@ -472,6 +484,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     // wrote whole: part_stride).
     if constexpr (Io::kStaleL1) asm volatile("buffer_inv sc1" ::: "memory");
     gqa_merge_heads<G, NW>(a, j, nact, tid, io);
+    trace_stamp(a.trace, kTraceGqaDecode, twg, 5);
   }
 }
 

@@ -532,6 +532,7 @@ __device__ void loop_a(const FusedArgs& a, unsigned tag, uint32_t* xs, int* flag
         d.angle_rows = a.angle_rows;
         d.nsplit = a.nsplit;
         d.scale_log2 = a.scale_log2;
+        d.trace = nullptr;
         FusedDecodeIo io{a, base + kOffQkv, base + kOffAtt, tag, xs, flag, kv};
         gqa_decode_chunk<kGQ, true, RES, 4>(d, s, j, pos, io);  // always reaches its input wait (flag[2])
         lds_barrier();

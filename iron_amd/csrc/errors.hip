@@ -19,6 +19,7 @@ void set_error(const char* fmt, ...) {
 
 int fail_einval(const char* fmt, ...) {
   disarm_timing();
+  disarm_trace();
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
@@ -28,6 +29,7 @@ int fail_einval(const char* fmt, ...) {
 
 int check_launch(const char* what) {
   disarm_timing();
+  disarm_trace();
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_error("%s: launch failed: %s", what, hipGetErrorString(e));
@@ -51,9 +53,36 @@ void disarm_timing() {
   g_timing_started = false;
 }
 
+struct TraceState {
+  void* buffer;
+  long long bytes;
+};
+static thread_local TraceState g_trace = {nullptr, 0};
+
+void disarm_trace() { g_trace = {nullptr, 0}; }
+
+int take_trace(const char* who, long long records, void** buffer) {
+  const TraceState t = g_trace;
+  disarm_trace();
+  *buffer = nullptr;
+  if (!t.buffer) return 0;
+  if (t.bytes < records * 64)
+    return fail_einval("%s: the armed trace buffer of %lld bytes holds %lld records; this launch writes %lld", who,
+                       t.bytes, t.bytes / 64, records);
+  *buffer = t.buffer;
+  return 0;
+}
+
 }  // namespace iron
 
 extern "C" const char* iron_last_error(void) { return iron::g_last_error; }
+
+extern "C" int iron_trace_next_launch(void* buffer, long long bytes) {
+  if (buffer && (bytes < 64 || (reinterpret_cast<uintptr_t>(buffer) & 63u)))
+    return iron::fail_einval("iron_trace_next_launch: the buffer must be 64-byte aligned and hold a record");
+  iron::g_trace = {buffer, buffer ? bytes : 0};
+  return 0;
+}
 
 extern "C" int iron_time_next_launch(void* start_event, void* stop_event) {
   if ((start_event == nullptr) != (stop_event == nullptr))

@@ -19,6 +19,7 @@
 //   residual : added to the (activated) result before the bf16 rounding
 #include "iron_common.hpp"
 #include "i4_dot.hpp"
+#include "trace.hpp"
 #include "../../include/iron_hip.h"
 
 namespace iron {
@@ -278,6 +279,7 @@ struct I4Args {
   float offset;    // 136 signed, 128 unsigned
   int xcd;         // 1: XCD-contiguous row order (xcd_block)
   unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
+  void* trace;      // phase trace records (trace.hpp), or null
 };
 
 // Fast path: K == 2048*GPL*KS. The 4 waves of a workgroup form 4/KS row
@@ -288,6 +290,8 @@ template <int GPL, int R, int KS, bool PAIR, int NM>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
   static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  // trace points: 0 start, 1 x prepared, 2 row products done
+  const unsigned long long t_start = trace_clock();
   const int tile = xcd_block(a.xcd);
   const int rg = wave / KS, kp = wave % KS;
   const int row0 = (tile * (4 / KS) + rg) * R;
@@ -345,6 +349,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) rres[r] = bf16_to_f32(a.resid ? a.resid[row0 + r] : a.x[0]);  // unconditional load
     __builtin_amdgcn_sched_barrier(0);
+    trace_write(a.trace, kTraceGemvI4, blockIdx.x, 0, t_start);
     if (NM != NORM_NONE) {
 #pragma unroll
       for (int j = 0; j < GPL; ++j)
@@ -375,6 +380,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
     // the compiler hoisted the scale conversions above it, and its wait for
     // them (counts are in issue order) also waited for every code load.
     __builtin_amdgcn_sched_barrier(0);
+    trace_stamp(a.trace, kTraceGemvI4, blockIdx.x, 1);
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -391,6 +397,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       part[r][0] = wave_sum(acc);
       part[r][1] = PAIR ? wave_sum(acc2) : 0.f;
     }
+    trace_stamp(a.trace, kTraceGemvI4, blockIdx.x, 2);
   }
   if (KS > 1) {  // K-split partners meet in LDS; the kp == 0 wave finishes the rows
     __shared__ float p_s[4][R][2];
@@ -493,14 +500,16 @@ __global__ __launch_bounds__(256) void gemv_i4_generic(I4Args a, int norm_mode) 
 }
 
 template <int GPL, int R, int KS, bool PAIR>
-void launch_i4_fast(const I4Args& a, int norm_mode, hipStream_t s) {
+int launch_i4_fast(I4Args a, int norm_mode, hipStream_t s) {
   const int rows_per_block = R * 4 / KS;
   dim3 grid((a.M + rows_per_block - 1) / rows_per_block), block(256);
+  if (int rc = take_trace("iron_gemv_i4g32", grid.x, &a.trace)) return rc;
   switch (norm_mode) {
     case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_WEIGHT>), grid, block, 0, s, a); break;
     case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_SCALE>), grid, block, 0, s, a); break;
     default: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_NONE>), grid, block, 0, s, a); break;
   }
+  return 0;
 }
 
 template <bool PAIR>
@@ -510,12 +519,13 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
   // they run many rounds of waves, each paying the load latency, so more bytes
   // in flight per wave pay (128256x2048: 1 row per wave 46 us, 2 rows 33 us,
   // 4 rows 27.5 us); at 8192 rows 4 per wave was 6% slower than 2.
+  int rc = 0;  // a refused trace request (take_trace)
   if (a.keys) {
-    if (a.K == 2048 && a.M % 4 == 0 && a.M >= 65536) launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
-    else if (a.K == 2048 && a.M % 2 == 0 && a.M >= 8192) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
-    else if (a.K == 2048) launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
+    if (a.K == 2048 && a.M % 4 == 0 && a.M >= 65536) rc = launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
+    else if (a.K == 2048 && a.M % 2 == 0 && a.M >= 8192) rc = launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
+    else if (a.K == 2048) rc = launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
     else IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
-    return check_launch("gemv_i4g32");
+    return rc ? rc : check_launch("gemv_i4g32");
   }
   // Two rows per wave share x when there are enough rows to keep >= 4 waves
   // per SIMD (for the SwiGLU pair, two rows of each matrix); longer rows are
@@ -524,15 +534,15 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
   switch (a.K) {
     case 2048:
       if (!PAIR && a.M % 4 == 0 && a.M >= 65536) {  // the lm_head shape: 31.3 -> 25.6 us
-        launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
+        rc = launch_i4_fast<1, 4, 1, PAIR>(a, norm_mode, s);
         break;
       }
-      if (r2) launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
-      else launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
+      if (r2) rc = launch_i4_fast<1, 2, 1, PAIR>(a, norm_mode, s);
+      else rc = launch_i4_fast<1, 1, 1, PAIR>(a, norm_mode, s);
       break;
     case 4096:  // a workgroup is 2 row groups: both must be inside M
       if (a.M % 2 == 0) {
-        launch_i4_fast<1, 1, 2, PAIR>(a, norm_mode, s);
+        rc = launch_i4_fast<1, 1, 2, PAIR>(a, norm_mode, s);
         break;
       }
       [[fallthrough]];
@@ -541,8 +551,8 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
         // One wave per row pair, four groups per lane (2048x8192 + residual with cold weights: 4.56 us,
         // against 4.69 with four waves splitting each row and 5.2 with two); the SwiGLU pair keeps four
         // waves per row.
-        if (!PAIR && a.M % 2 == 0) launch_i4_fast<4, 2, 1, PAIR>(a, norm_mode, s);
-        else launch_i4_fast<1, 1, 4, PAIR>(a, norm_mode, s);
+        if (!PAIR && a.M % 2 == 0) rc = launch_i4_fast<4, 2, 1, PAIR>(a, norm_mode, s);
+        else rc = launch_i4_fast<1, 1, 4, PAIR>(a, norm_mode, s);
         break;
       }
       [[fallthrough]];
@@ -550,7 +560,7 @@ int launch_gemv_i4(const I4Args& a, int norm_mode, hipStream_t s) {
       IRON_LAUNCH((gemv_i4_generic<PAIR>), dim3((a.M + 3) / 4), dim3(256), 0, s, a, norm_mode);
       break;
   }
-  return check_launch("gemv_i4g32");
+  return rc ? rc : check_launch("gemv_i4g32");
 }
 
 // ---------------------------------------------------------------------------

@@ -239,6 +239,13 @@ struct TimingEvents {
 };
 TimingEvents take_timing_events();  // events for this launch (start only on the first)
 void disarm_timing();               // end of an entry point (called by check_launch)
+// Device phase trace armed by iron_trace_next_launch() for this thread's next
+// entry-point call. An entry point whose kernel carries trace points asks for
+// `records` 64-byte records (one per workgroup): *buffer receives the armed
+// buffer (nullptr when tracing is off), and the trace is disarmed. Returns
+// IRON_EINVAL (error set) when the armed buffer is too small.
+int take_trace(const char* who, long long records, void** buffer);
+void disarm_trace();  // end of an entry point (check_launch, fail_einval)
 // 1 when workgroups whose linear ids agree mod 8 run on one XCD of the current
 // device (checked once per device, then cached); 0 when they do not, or when
 // it cannot be checked now (`stream` is being captured).

@@ -27,9 +27,9 @@
 // Pairs left by an earlier call carry an older tag and are never accepted.
 //
 // Bounded waits: a gather that does not see its pairs within wait_us, or sees
-// a nonzero status word, gives up; it sets status bit 1, its workgroup skips
-// its output rows, and every later wait (this call or the next) sees the
-// status and gives up at once. The caller checks the word and, after a
+// a nonzero status word (read with every round of its loads), gives up; it
+// sets status bit 1, its workgroup skips its output rows, and every later wait
+// (this call or the next) sees the status and gives up at once. The caller checks the word and, after a
 // give-up, zero-fills the workspace before the next call.
 //
 // Arithmetic. The per-row sums are those of the two separate GEMVs
@@ -40,6 +40,7 @@
 #include "iron_common.hpp"
 #include "i4_dot.hpp"
 #include "exchange.hpp"
+#include "trace.hpp"
 #include "../../include/iron_hip.h"
 
 namespace iron {
@@ -79,12 +80,15 @@ struct SwArgs {
   uint32_t magic;  // i4_dot.hpp: signed or unsigned codes
   float offset;
   unsigned wait_ticks;  // 100 MHz
+  void* trace;          // phase trace records (trace.hpp), or null
 };
 
 template <int NM>
 __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t h_s[kSwPairs];  // h as bf16 pairs
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  // trace points: 0 start, 1 x ready, 2 h published, 3 h gathered, 4 down row done
+  const unsigned long long t_start = trace_clock();
   const int blk = xcd_block(1);  // each XCD owns a contiguous eighth of the units and rows
   unsigned* status = reinterpret_cast<unsigned*>(a.ws + kSwStatusOff);
   unsigned* epoch = reinterpret_cast<unsigned*>(a.ws + kSwEpochOff);
@@ -130,6 +134,7 @@ __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwAr
   const float rres = bf16_to_f32(a.resid ? a.resid[dr] : a.x[0]);  // unconditional load
   // keeps the scheduler from sinking any of these loads below the products
   __builtin_amdgcn_sched_barrier(0);
+  trace_write(a.trace, kTraceSwigluDecode, blockIdx.x, 0, t_start);
 
   // The wave's four FFN units (the pair GEMV's arithmetic, one group per lane).
   float inv = 1.f;
@@ -139,6 +144,7 @@ __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwAr
     for (int q = 0; q < 4; ++q) ss = sumsq_chunk(xq[q], ss);
     inv = inv_rms(wave_sum(ss), kSwE, a.eps);
   }
+  trace_stamp(a.trace, kTraceSwigluDecode, blockIdx.x, 1);
   if (NM == SW_NORM_WEIGHT) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) xq[q] = normalize_chunk(xq[q], nq[q], inv);
@@ -162,32 +168,49 @@ __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwAr
       hv[i >> 1] = h;
   }
   if (lane == 0) st_pairs2(xr, u0 / 2, hv[0], hv[1], tag);
+  trace_stamp(a.trace, kTraceSwigluDecode, blockIdx.x, 2);
 
   // Gather every h value (4096 pairs: four 16-byte loads per thread) into LDS.
-  bool ok = true;
+  // One round trip per retry: the pairs still missing are loaded again
+  // together with the status word (lane 0 of each wave), and the wave retries
+  // until every lane holds its pairs, the status is nonzero, or wait_us passes.
+  bool ok = true;  // wave-uniform
   {
     u32x4_v v[kSwGatherLoads];
 #pragma unroll
     for (int k = 0; k < kSwGatherLoads; ++k) v[k] = ld_pairs2(xr, 2 * (tid + kSwWaves * kWave * k));
+    unsigned st = lane == 0 ? read_status(status) : 0u;
+    const unsigned long long t0 = now_ticks();
+    unsigned got = 0;  // bit k: the pairs of load k are in LDS
+    for (;;) {
 #pragma unroll
-    for (int k = 0; k < kSwGatherLoads; ++k) {
-      const int p = 2 * (tid + kSwWaves * kWave * k);
-      if (v[k][1] != tag || v[k][3] != tag) {  // not there yet: poll this pair of pairs
-        const unsigned long long t0 = now_ticks();
-        while (ok && (v[k][1] != tag || v[k][3] != tag)) {
-          if (read_status(status) != 0u || now_ticks() - t0 > a.wait_ticks) ok = false;
-          __builtin_amdgcn_s_sleep(1);
-          v[k] = ld_pairs2(xr, p);
+      for (int k = 0; k < kSwGatherLoads; ++k)
+        if (!(got & (1u << k)) && v[k][1] == tag && v[k][3] == tag) {
+          *reinterpret_cast<uint2*>(&h_s[2 * (tid + kSwWaves * kWave * k)]) = make_uint2(v[k][0], v[k][2]);
+          got |= 1u << k;
         }
+      if (__builtin_amdgcn_ballot_w64(st != 0u)) {
+        ok = false;
+        break;
       }
-      *reinterpret_cast<uint2*>(&h_s[p]) = make_uint2(v[k][0], v[k][2]);
+      if (!__builtin_amdgcn_ballot_w64(got != (1u << kSwGatherLoads) - 1)) break;
+      if (now_ticks() - t0 > a.wait_ticks) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int k = 0; k < kSwGatherLoads; ++k)
+        if (!(got & (1u << k))) v[k] = ld_pairs2(xr, 2 * (tid + kSwWaves * kWave * k));
+      if (lane == 0) st = read_status(status);
     }
   }
-  if (!ok) give_up(status, 1u);
-  const int failed = __syncthreads_or(!ok || (tid == 0 && read_status(status) != 0u));
+  if (!ok && lane == 0) give_up(status, 1u);
+  const int failed = __syncthreads_or(!ok);
   // Every workgroup has read the epoch (each published its pairs after doing so).
   if (blockIdx.x == 0 && tid == 0) *epoch = (e + 1u == 0xffffffffu) ? 0u : e + 1u;
   if (failed) return;
+  trace_stamp(a.trace, kTraceSwigluDecode, blockIdx.x, 3);
 
   // The wave's down row against h (the down GEMV's arithmetic).
   const uint4* hq = reinterpret_cast<const uint4*>(h_s);
@@ -203,6 +226,7 @@ __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwAr
   }
   const float t = wave_sum(acc);
   if (lane == 0) a.y[dr] = f32_to_bf16(a.resid ? t + rres : t);
+  trace_stamp(a.trace, kTraceSwigluDecode, blockIdx.x, 4);
 }
 
 }  // namespace
@@ -285,6 +309,7 @@ extern "C" int iron_swiglu_decode_i4g32(const void* gate_codes, const void* gate
   a.magic = is_signed ? 0x43084308u : 0x43004300u;
   a.offset = is_signed ? 136.f : 128.f;
   a.wait_ticks = wait_us * 100u;
+  if (int rc = take_trace(who, kSwGrid, &a.trace)) return rc;
   const dim3 g(kSwGrid), blk(kSwWaves * kWave);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (norm_mode) {

@@ -26,6 +26,8 @@ class GEMVInt4(HIPOperator):
     group_size: int = 32
     signed: bool = field(default=True, repr=False)
     context: object = field(default=None, repr=False)
+    # bytes of the per-call device phase trace (iron_amd/common/tracing_utils.py); None: IRON_TRACE_SIZE
+    trace_size: int | None = field(default=None, repr=False)
 
     def __post_init__(self):
         if self.group_size != 32:

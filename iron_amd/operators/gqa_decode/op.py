@@ -35,6 +35,8 @@ class GQADecode(HIPOperator):
     scale: float | None = field(default=None, repr=False)
     position_parameter: str | None = field(default=None, repr=False)
     context: object = field(default=None, repr=False)
+    # bytes of the per-call device phase trace (iron_amd/common/tracing_utils.py); None: IRON_TRACE_SIZE
+    trace_size: int | None = field(default=None, repr=False)
 
     def __post_init__(self):
         if self.head_dim != 64:

@@ -17,8 +17,9 @@ from iron_amd import _lib  # noqa: E402  (the argument tables only; the GPU libr
 
 EINVAL = 22
 # entry points with no argument to refuse: iron_time_next_launch takes two event
-# handles (NULL, NULL disarms; others arm), which it only records
-NO_CHECKS = {"iron_time_next_launch"}
+# handles (NULL, NULL disarms; others arm), which it only records;
+# iron_trace_next_launch takes NULL as "disarm" (its alignment check is called below)
+NO_CHECKS = {"iron_time_next_launch", "iron_trace_next_launch"}
 
 
 def _args(argtypes, ptr, i, f):
@@ -53,6 +54,11 @@ def main() -> int:
             assert rc == EINVAL, (name, ptr, rc)
             msg = lib.iron_last_error()
             assert msg and len(msg) > 8, (name, msg)  # a description of what was refused
+    tr = lib.iron_trace_next_launch
+    tr.restype, tr.argtypes = ctypes.c_int, _lib.SIGNATURES["iron_trace_next_launch"]
+    assert tr((1 << 20) + 16, 4096) == EINVAL and lib.iron_last_error()
+    assert tr(None, 0) == 0
+    calls += 2
     for name, (restype, argtypes) in _lib.QUERIES.items():
         fn = getattr(lib, name)
         fn.restype = restype
