@@ -1101,7 +1101,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": int(traffic) if traffic else None,
-            "kernel": "gemv_i4_fast<1, 2, 1, false, 0>",
+            "kernel": "gemv_i4_fast<1, 2, 1, false, 0, false>",
             "kernel_us": round(kernel_us_roof, 3),
             "kernel_us_source": TRACE_PROFILE if trace_ns else "live (profile missing)",
             "traffic_source": PMC_PROFILE if traffic else None,

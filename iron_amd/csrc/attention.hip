@@ -465,7 +465,7 @@ static bool decode_long_chunks(int n_kv_heads, int max_len, int pos, bool reside
   return (resident ? 2 * active : active) >= device_cus();
 }
 
-template <int G, bool RES>
+template <int G, bool RES, bool TR>
 static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_launch, bool long_chunks, hipStream_t s) {
   const dim3 block(kDecThreads);
   if (one_launch) {
@@ -473,14 +473,24 @@ static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_la
     DecodeArgs b = a;
     b.nsplit = (a.max_len + 16 * kDecWaves1 - 1) / (16 * kDecWaves1);
     if (long_chunks)
-      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1>), dim3(b.nsplit * n_kv_heads), dim3(kDecWaves1 * kWave),
-                  0, s, b);
+      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1, TR>), dim3(b.nsplit * n_kv_heads),
+                  dim3(kDecWaves1 * kWave), 0, s, b);
     else
-      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, 4>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
+      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, 4, TR>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
   } else {
-    IRON_LAUNCH((gqa_decode_kernel<G, false, RES, 4>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
+    IRON_LAUNCH((gqa_decode_kernel<G, false, RES, 4, TR>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
     IRON_LAUNCH((gqa_combine_kernel<G>), dim3(n_kv_heads * G), dim3(kMergeThreads), 0, s, a);
   }
+}
+
+// The traced instance only while a phase trace is armed.
+template <int G, bool RES>
+static void gqa_decode_dispatch_tr(const DecodeArgs& a, int n_kv_heads, bool one_launch, bool long_chunks,
+                                   hipStream_t s) {
+  if (a.trace)
+    gqa_decode_dispatch<G, RES, true>(a, n_kv_heads, one_launch, long_chunks, s);
+  else
+    gqa_decode_dispatch<G, RES, false>(a, n_kv_heads, one_launch, long_chunks, s);
 }
 
 static int gqa_decode_launch(const char* who, const void* q, const void* k_new, const void* v_new, void* k_cache,
@@ -530,17 +540,17 @@ static int gqa_decode_launch(const char* who, const void* q, const void* k_new, 
     IRON_LAUNCH(gqa_clear_counters_kernel, dim3(1), dim3(kWave), 0, s, a.ctr, n_kv_heads);
   if (flags & IRON_GQA_KV_RESIDENT) {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, true>(a, n_kv_heads, one, long_chunks, s); break;
-      case 2: gqa_decode_dispatch<2, true>(a, n_kv_heads, one, long_chunks, s); break;
-      case 4: gqa_decode_dispatch<4, true>(a, n_kv_heads, one, long_chunks, s); break;
-      default: gqa_decode_dispatch<8, true>(a, n_kv_heads, one, long_chunks, s); break;
+      case 1: gqa_decode_dispatch_tr<1, true>(a, n_kv_heads, one, long_chunks, s); break;
+      case 2: gqa_decode_dispatch_tr<2, true>(a, n_kv_heads, one, long_chunks, s); break;
+      case 4: gqa_decode_dispatch_tr<4, true>(a, n_kv_heads, one, long_chunks, s); break;
+      default: gqa_decode_dispatch_tr<8, true>(a, n_kv_heads, one, long_chunks, s); break;
     }
   } else {
     switch (G) {
-      case 1: gqa_decode_dispatch<1, false>(a, n_kv_heads, one, long_chunks, s); break;
-      case 2: gqa_decode_dispatch<2, false>(a, n_kv_heads, one, long_chunks, s); break;
-      case 4: gqa_decode_dispatch<4, false>(a, n_kv_heads, one, long_chunks, s); break;
-      default: gqa_decode_dispatch<8, false>(a, n_kv_heads, one, long_chunks, s); break;
+      case 1: gqa_decode_dispatch_tr<1, false>(a, n_kv_heads, one, long_chunks, s); break;
+      case 2: gqa_decode_dispatch_tr<2, false>(a, n_kv_heads, one, long_chunks, s); break;
+      case 4: gqa_decode_dispatch_tr<4, false>(a, n_kv_heads, one, long_chunks, s); break;
+      default: gqa_decode_dispatch_tr<8, false>(a, n_kv_heads, one, long_chunks, s); break;
     }
   }
   return check_launch(who);

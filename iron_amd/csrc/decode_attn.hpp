@@ -253,7 +253,9 @@ struct PlainDecodeIo {
 template <int G, int NW, class Io>
 __device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, const Io& io);
 
-template <int G, bool MERGE, bool RES, int NW, class Io>
+// TR: the instance launched while a phase trace is armed (trace.hpp); the
+// others carry no trace code.
+template <int G, bool MERGE, bool RES, int NW, class Io, bool TR = false>
 __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int j, int pos, Io& io) {
   constexpr int D = kD;
   constexpr int NT = NW * kWave;   // threads
@@ -268,7 +270,9 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // trace points: 0 start, 1 q in LDS, 2 scores and P V done, 3 partial stored
   // (acknowledged on the one-launch path), 4 counted in, 5 merged (last arriver)
   const unsigned twg = blockIdx.x + blockIdx.y * gridDim.x;
-  const unsigned long long t_start = trace_clock();
+  void* const trace = TR ? a.trace : nullptr;
+  unsigned long long t_start = 0;
+  if constexpr (TR) t_start = trace_clock();
   if (pos < 0 || pos >= a.max_len || pos >= a.angle_rows) return;  // rejected on the host when pos is known
   const int L = pos + 1;
   const int p0 = s * CH;
@@ -316,7 +320,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // K/V loads are ordinary, allocating loads (decode +0.9%). Otherwise they are
   // streaming loads, faster when the caches come from HBM every time.
   const DecodeKv kv = io.template kv_rows<RES>(a, p0, j);
-  trace_write(a.trace, kTraceGqaDecode, twg, 0, t_start);
+  trace_write(trace, kTraceGqaDecode, twg, 0, t_start);
   uint4 k0 = kv.k0, k1 = kv.k1;
   unsigned char* vblk = v_s[w];
   const uint4 vraw[2] = {kv.v0, kv.v1};
@@ -337,7 +341,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   // barrier without a wait for the K/V loads in flight (__syncthreads would
   // wait for all of them); the memory clobber keeps the q_s accesses on their sides
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  trace_stamp(a.trace, kTraceGqaDecode, twg, 1);
+  trace_stamp(trace, kTraceGqaDecode, twg, 1);
   const int hq = r & (G - 1);
   const dec_bf16x8 qb0 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + cq * 8]);
   const dec_bf16x8 qb1 = *reinterpret_cast<const dec_bf16x8*>(&q_s[hq * D + (cq + 4) * 8]);
@@ -441,7 +445,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
   else
     wave_body(std::false_type{});
   __syncthreads();
-  trace_stamp(a.trace, kTraceGqaDecode, twg, 2);
+  trace_stamp(trace, kTraceGqaDecode, twg, 2);
 
   // the chunk's partial: the four waves merged
   float* part = a.part + static_cast<size_t>(j) * a.head_stride + static_cast<size_t>(s) * PS;
@@ -460,13 +464,13 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     part[t] = o;
     if (t % D == 0) *reinterpret_cast<float2*>(part + G * D + 2 * g) = make_float2(M, l);
   }
-  if constexpr (!MERGE) trace_stamp(a.trace, kTraceGqaDecode, twg, 3);
+  if constexpr (!MERGE) trace_stamp(trace, kTraceGqaDecode, twg, 3);
   if constexpr (MERGE) {
     __shared__ int last_s;
     const int nact = (L + CH - 1) / CH;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have reached the L2
     __syncthreads();
-    trace_stamp(a.trace, kTraceGqaDecode, twg, 3);
+    trace_stamp(trace, kTraceGqaDecode, twg, 3);
     if (tid == 0) {  // an atomic in the XCD's L2, where the partials are
       unsigned* c = a.ctr + static_cast<size_t>(j) * kCtrStride;
       const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -475,7 +479,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
       last_s = last;
     }
     __syncthreads();
-    trace_stamp(a.trace, kTraceGqaDecode, twg, 4);
+    trace_stamp(trace, kTraceGqaDecode, twg, 4);
     if (!last_s) return;
     // An Io whose persistent workgroups merge again later (Io::kStaleL1) may
     // hold lines of an earlier merge's partials in this CU's L1: an
@@ -484,7 +488,7 @@ __device__ __forceinline__ void gqa_decode_chunk(const DecodeArgs& a, int s, int
     // wrote whole: part_stride).
     if constexpr (Io::kStaleL1) asm volatile("buffer_inv sc1" ::: "memory");
     gqa_merge_heads<G, NW>(a, j, nact, tid, io);
-    trace_stamp(a.trace, kTraceGqaDecode, twg, 5);
+    trace_stamp(trace, kTraceGqaDecode, twg, 5);
   }
 }
 
@@ -577,7 +581,7 @@ __device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, c
   }
 }
 
-template <int G, bool MERGE, bool RES, int NW>
+template <int G, bool MERGE, bool RES, int NW, bool TR>
 __global__ __launch_bounds__(NW * kWave) void gqa_decode_kernel(DecodeArgs a) {
   int s, j;
   if constexpr (MERGE) {
@@ -589,7 +593,7 @@ __global__ __launch_bounds__(NW * kWave) void gqa_decode_kernel(DecodeArgs a) {
     j = blockIdx.y;
   }
   PlainDecodeIo<G> io{a};
-  gqa_decode_chunk<G, MERGE, RES, NW>(a, s, j, a.pos_dev ? *a.pos_dev : a.pos, io);
+  gqa_decode_chunk<G, MERGE, RES, NW, PlainDecodeIo<G>, TR>(a, s, j, a.pos_dev ? *a.pos_dev : a.pos, io);
 }
 
 // Merge of the chunk partials, one 1024-thread workgroup per query head

@@ -17,6 +17,8 @@
 //   W2       : a second matrix of the same shape; the output is
 //              silu(W.x) * (W2.x)   (the SwiGLU gate/up pair)
 //   residual : added to the (activated) result before the bf16 rounding
+#include <type_traits>
+
 #include "iron_common.hpp"
 #include "i4_dot.hpp"
 #include "trace.hpp"
@@ -286,12 +288,17 @@ struct I4Args {
 // groups of R rows; the KS waves of a row group split K, each lane owning GPL
 // groups of 32 per row, and their partial sums meet in LDS. R rows of one
 // wave share the x preparation.
-template <int GPL, int R, int KS, bool PAIR, int NM>
+// TR: the instance launched while a phase trace is armed (trace.hpp); the
+// others carry no trace code, whose clock read at entry measured 0.1 us of the
+// headline launch.
+template <int GPL, int R, int KS, bool PAIR, int NM, bool TR>
 __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
   static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   // trace points: 0 start, 1 x prepared, 2 row products done
-  const unsigned long long t_start = trace_clock();
+  void* const trace = TR ? a.trace : nullptr;
+  unsigned long long t_start = 0;
+  if constexpr (TR) t_start = trace_clock();
   const int tile = xcd_block(a.xcd);
   const int rg = wave / KS, kp = wave % KS;
   const int row0 = (tile * (4 / KS) + rg) * R;
@@ -349,7 +356,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) rres[r] = bf16_to_f32(a.resid ? a.resid[row0 + r] : a.x[0]);  // unconditional load
     __builtin_amdgcn_sched_barrier(0);
-    trace_write(a.trace, kTraceGemvI4, blockIdx.x, 0, t_start);
+    trace_write(trace, kTraceGemvI4, blockIdx.x, 0, t_start);
     if (NM != NORM_NONE) {
 #pragma unroll
       for (int j = 0; j < GPL; ++j)
@@ -380,7 +387,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
     // the compiler hoisted the scale conversions above it, and its wait for
     // them (counts are in issue order) also waited for every code load.
     __builtin_amdgcn_sched_barrier(0);
-    trace_stamp(a.trace, kTraceGemvI4, blockIdx.x, 1);
+    trace_stamp(trace, kTraceGemvI4, blockIdx.x, 1);
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -397,7 +404,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
       part[r][0] = wave_sum(acc);
       part[r][1] = PAIR ? wave_sum(acc2) : 0.f;
     }
-    trace_stamp(a.trace, kTraceGemvI4, blockIdx.x, 2);
+    trace_stamp(trace, kTraceGemvI4, blockIdx.x, 2);
   }
   if (KS > 1) {  // K-split partners meet in LDS; the kp == 0 wave finishes the rows
     __shared__ float p_s[4][R][2];
@@ -504,11 +511,18 @@ int launch_i4_fast(I4Args a, int norm_mode, hipStream_t s) {
   const int rows_per_block = R * 4 / KS;
   dim3 grid((a.M + rows_per_block - 1) / rows_per_block), block(256);
   if (int rc = take_trace("iron_gemv_i4g32", grid.x, &a.trace)) return rc;
-  switch (norm_mode) {
-    case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_WEIGHT>), grid, block, 0, s, a); break;
-    case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_SCALE>), grid, block, 0, s, a); break;
-    default: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_NONE>), grid, block, 0, s, a); break;
-  }
+  auto go = [&](auto tr) {
+    constexpr bool TR = decltype(tr)::value;
+    switch (norm_mode) {
+      case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_WEIGHT, TR>), grid, block, 0, s, a); break;
+      case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_SCALE, TR>), grid, block, 0, s, a); break;
+      default: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_NONE, TR>), grid, block, 0, s, a); break;
+    }
+  };
+  if (a.trace)
+    go(std::true_type{});
+  else
+    go(std::false_type{});
   return 0;
 }
 

@@ -5,11 +5,13 @@
 //                     shared by every XCD), k < kTraceStamps
 // Stamp k is the moment the workgroup's wave 0 passed the kernel's k-th trace
 // point; a point the workgroup never reaches stays as the caller zero-filled
-// it. With no buffer armed every trace point is one uniform branch on a kernel
-// argument, except that the start clock is read unconditionally at entry
-// (trace_clock) and recorded later (trace_write): a test of the trace pointer
-// at entry would make the kernel wait for that argument before it issues its
-// other argument loads.
+// it. Kernels on the decode path have a separate traced instance, launched
+// only while a buffer is armed (their untraced instance holds no trace code: a
+// clock read at entry measured 0.1 us on the int4 GEMV). In a kernel without
+// one, each trace point is a uniform branch on the trace pointer, and the
+// start clock is read unconditionally at entry (trace_clock) and recorded
+// later (trace_write): a test of the trace pointer at entry would make the
+// kernel wait for that argument before it issues its other argument loads.
 #pragma once
 
 #include "iron_common.hpp"
