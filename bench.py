@@ -560,8 +560,9 @@ def _traced(torch, dev, launch, copies, calls, tag):
 
 def bench_trace(torch, lib, dev, calls=25):
     """--mode trace: per-workgroup phase traces of the decode attention (config
-    3 and KV 4096, streamed caches), the headline int4 GEMV (config 2) and the
-    one-launch SwiGLU block (config 4), on cold inputs."""
+    3 and KV 4096, streamed caches), the headline int4 GEMV (config 2), the
+    one-launch SwiGLU block (config 4) and the bf16 prefill GEMM (config 5 and
+    4096^3), on cold inputs."""
     from iron_amd import _lib
     from oracle import configs, ops
 
@@ -625,6 +626,22 @@ def bench_trace(torch, lib, dev, calls=25):
     res["swiglu_one_launch_cfg4"] = _traced(torch, dev, swiglu, copies, calls, "swiglu_one_launch_cfg4")
     if int(ws[:4].view(torch.int32).item()) != 0:
         raise RuntimeError("iron_swiglu_decode_i4g32: a wait gave up during the trace")
+    del Q
+    # the bf16 prefill GEMM: config 5 (128x128 tiles, one per CU) and 4096^3 (256x256 tiles), cold weights
+    for tag, (M, K, N) in (("gemm_cfg5", (512, 2048, 8192)), ("gemm_4096", (4096, 4096, 4096))):
+        g = torch.Generator(device=dev).manual_seed(0)
+        A = torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16)
+        W = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        C = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        copies = copies_for(2 * W.numel())
+        Ws = [W] + [W.clone() for _ in range(copies - 1)]
+
+        def gemm(i, s):
+            _check(lib, lib.iron_gemm_bf16_nt(A.data_ptr(), Ws[i % copies].data_ptr(), C.data_ptr(), M, N, K, N, 0, 0,
+                                              0.0, 0.0, s))
+
+        res[tag] = _traced(torch, dev, gemm, copies, calls, tag)
+        del Ws
     return res
 
 

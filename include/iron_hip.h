@@ -46,10 +46,11 @@ int iron_time_next_launch(void* start_event, void* stop_event);
  * iron/common/tracing_utils.py:49-115 turns into Perfetto JSON and a cycles
  * summary. Kernels with trace points (iron_gqa_decode and its variants,
  * iron_gemv_i4g32 and iron_gemv_i4g32_fused on their fast path,
- * iron_swiglu_decode_i4g32) write one 64-byte record per workgroup into
+ * iron_swiglu_decode_i4g32, the bf16 GEMM entry points) write one 64-byte
+ * record per workgroup into
  * `buffer` (device memory, 64-byte aligned, zero-filled by the caller), from
  * the workgroup's first thread, at record index = the workgroup's linear id:
- *   uint32 kernel id (1 gqa_decode, 2 gemv_i4, 3 swiglu_decode_i4),
+ *   uint32 kernel id (1 gqa_decode, 2 gemv_i4, 3 swiglu_decode_i4, 4 gemm_bf16),
  *   uint32 workgroup, uint32 XCC_ID, uint32 HW_ID register,
  *   uint64 stamps[6]: s_memrealtime (100 MHz, one clock for every XCD) when
  *   the workgroup passed each of the kernel's trace points (0 where it did

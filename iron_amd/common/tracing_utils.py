@@ -8,7 +8,7 @@ trace text, Perfetto JSON and a cycles summary.
 Here the trace is written by the kernels themselves. ``iron_trace_next_launch``
 (include/iron_hip.h) arms a device buffer for the next entry-point call. Kernels
 with trace points (decode attention, the int4 GEMV fast path, the one-launch
-SwiGLU block) then write one 64-byte record per workgroup: kernel id,
+SwiGLU block, the bf16 GEMM) then write one 64-byte record per workgroup: kernel id,
 workgroup, XCC_ID, HW_ID, and up to six s_memrealtime stamps (100 MHz, one
 clock for all XCDs) taken when the workgroup passed each trace point.
 
@@ -56,6 +56,7 @@ KERNELS = {
     1: ("gqa_decode", ("start", "q in LDS", "scores and P.V", "partial stored", "counted in", "merged")),
     2: ("gemv_i4", ("start", "x prepared", "row products")),
     3: ("swiglu_decode_i4", ("start", "x ready", "h published", "h gathered", "down row")),
+    4: ("gemm_bf16", ("start", "first stage", "K quarter", "K half", "K three quarters", "tile stored")),
 }
 
 

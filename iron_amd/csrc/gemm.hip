@@ -42,6 +42,7 @@
 #include <algorithm>
 
 #include "iron_common.hpp"
+#include "trace.hpp"
 #include "../../include/iron_hip.h"
 
 namespace iron {
@@ -88,6 +89,7 @@ struct GemmArgs {
   const uint16_t* scales;
   int is_signed;
   int toward_zero;  // output-stage conversions truncate instead of rounding to nearest even
+  void* trace;      // phase trace records (trace.hpp), read by the traced instance only
 };
 
 // Splits an entry point's epilogue code into the activation (a.epi) and the
@@ -314,10 +316,16 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int b, int& kb, i
   tm = t % tiles_m, tn = t / tiles_m;
 }
 
-template <class T>
+// TR: the instance launched while a phase trace is armed (trace.hpp); the
+// others carry no trace code. Trace points: 0 start, 1 first stage in LDS,
+// 2-4 after a quarter, half and three quarters of the K steps, 5 tile stored.
+template <class T, bool TR>
 __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
   constexpr int BM = T::BM, BN = T::BN, TI = T::TI, TJ = T::TJ, NS = T::NS, PW = T::kPerWave;
   __shared__ u32x4v smem[NS * T::kStage];
+  void* const trace = TR ? a.trace : nullptr;
+  unsigned long long t_start = 0;
+  if constexpr (TR) t_start = trace_clock();
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / T::WNW, wn = wave % T::WNW;
@@ -375,11 +383,13 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p)
     if (p < nk) issue(p);
+  trace_write(trace, kTraceGemm, blockIdx.x, 0, t_start);
   if (NS - 1 < nk)
     wait_loads_barrier<PW * (NS - 2)>();
   else
     wait_loads_barrier<0>();
   read_frags(0, 0, 0);
+  trace_stamp(trace, kTraceGemm, blockIdx.x, 1);
 
   // One step; LAST: the range's last step (no barrier, no next fragments). The
   // last step is peeled off so that the other steps' final k-slice has one
@@ -419,10 +429,17 @@ __global__ __launch_bounds__(T::kThreads) void gemm_nt_kernel(GemmArgs a) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
     }
   };
-  for (int s = 0; s + 1 < nk; ++s) step(s, std::false_type{});
+  for (int s = 0; s + 1 < nk; ++s) {
+    step(s, std::false_type{});
+    if constexpr (TR) {
+      if (4 * (s + 1) == nk || 2 * (s + 1) == nk || 4 * (s + 1) == 3 * nk)
+        trace_stamp(trace, kTraceGemm, blockIdx.x, 4 * (s + 1) == nk ? 2 : 2 * (s + 1) == nk ? 3 : 4);
+    }
+  }
   step(nk - 1, std::true_type{});
 
   store_tile<T>(a, acc, smem, m0, n0, kb, wm, wn, lane, tid);
+  trace_stamp(trace, kTraceGemm, blockIdx.x, 5);
 }
 
 // ---------------------------------------------------------------------------
@@ -746,8 +763,14 @@ static double launch_cost(const GemmArgs& a, int per_cu, double tflops) {
 }
 
 template <class T>
-static void launch_tile(const GemmArgs& a, hipStream_t s) {
-  IRON_LAUNCH(gemm_nt_kernel<T>, dim3(static_cast<unsigned>(tile_count<T>(a))), dim3(T::kThreads), 0, s, a);
+static int launch_tile(GemmArgs a, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(tile_count<T>(a)));
+  if (int rc = take_trace("gemm", grid.x, &a.trace)) return rc;
+  if (a.trace)
+    IRON_LAUNCH((gemm_nt_kernel<T, true>), grid, dim3(T::kThreads), 0, s, a);
+  else
+    IRON_LAUNCH((gemm_nt_kernel<T, false>), grid, dim3(T::kThreads), 0, s, a);
+  return 0;
 }
 
 template <class T>
@@ -768,18 +791,12 @@ static int small_tile(int M, int N) {
   return 0;
 }
 
-static void gemm_launch(const GemmArgs& a, hipStream_t s) {
+static int gemm_launch(const GemmArgs& a, hipStream_t s) {
   // The SwiGLU pair needs 128-column tiles.
   if (a.splits == 1 && a.epi != kEpiSwigluPair) {
     const int st = small_tile(a.M, a.N);
-    if (st == 64) {
-      launch_tile<Tile64>(a, s);
-      return;
-    }
-    if (st == 128) {
-      launch_tile<Tile128x64>(a, s);
-      return;
-    }
+    if (st == 64) return launch_tile<Tile64>(a, s);
+    if (st == 128) return launch_tile<Tile128x64>(a, s);
   }
   const double cl = launch_cost<TileL>(a, 1, 1000.0), cm = launch_cost<TileM>(a, 1, 900.0);
   const double cs = launch_cost<TileS>(a, 1, 660.0), cs2 = launch_cost<TileS2>(a, 2, 800.0);
@@ -789,15 +806,15 @@ static void gemm_launch(const GemmArgs& a, hipStream_t s) {
   const double cl3 = (a.N % TileL3::BN == 0 && a.epi != kEpiSwigluPair) ? launch_cost<TileL3>(a, 1, 900.0) : 1e300;
   const double best = std::min(std::min(std::min(cl, cm), std::min(cs, cs2)), cl3);
   if (cl3 == best)
-    launch_tile<TileL3>(a, s);
+    return launch_tile<TileL3>(a, s);
   else if (cs == best)
-    launch_tile<TileS>(a, s);
+    return launch_tile<TileS>(a, s);
   else if (cl == best)
-    launch_tile<TileL>(a, s);
+    return launch_tile<TileL>(a, s);
   else if (cm == best)
-    launch_tile<TileM>(a, s);
+    return launch_tile<TileM>(a, s);
   else
-    launch_tile<TileS2>(a, s);
+    return launch_tile<TileS2>(a, s);
 }
 
 extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, int N, int K, long long ldc,
@@ -809,7 +826,7 @@ extern "C" int iron_gemm_bf16_nt(const void* A, const void* B, void* C, int M, i
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(B), static_cast<uint16_t*>(C), M, N, K,
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, nullptr, 1};
   set_epilogue(a, epilogue);
-  gemm_launch(a, static_cast<hipStream_t>(stream));
+  if (int rc = gemm_launch(a, static_cast<hipStream_t>(stream))) return rc;
   return check_launch("gemm_bf16_nt");
 }
 
@@ -888,7 +905,7 @@ extern "C" int iron_gemm_bf16_nt_splitk(const void* A, const void* B, void* C, i
              ldc, epilogue, has_clamp, clamp_lo, clamp_hi, static_cast<float*>(workspace), splits};
   set_epilogue(a, epilogue);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  gemm_launch(a, s);
+  if (int rc = gemm_launch(a, s)) return rc;
   launch_splitk_reduce(a, s);
   return check_launch("gemm_bf16_nt_splitk");
 }
@@ -904,7 +921,7 @@ extern "C" int iron_gemm_bf16_nt_swiglu(const void* A, const void* Bgu, void* H,
   IRON_REQUIRE(tiles < (1LL << 31), "iron_gemm_bf16_nt_swiglu: problem too large");
   GemmArgs a{static_cast<const uint16_t*>(A), static_cast<const uint16_t*>(Bgu), static_cast<uint16_t*>(H), M, 2 * F,
              K, ldh, kEpiSwigluPair, 0, 0.f, 0.f, nullptr, 1};
-  gemm_launch(a, static_cast<hipStream_t>(stream));
+  if (int rc = gemm_launch(a, static_cast<hipStream_t>(stream))) return rc;
   return check_launch("gemm_bf16_nt_swiglu");
 }
 
@@ -974,8 +991,8 @@ extern "C" int iron_gemm_nt_partials(const void* A, const void* B, const void* c
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (i4)
     gemm_i4_launch(a, s);
-  else
-    gemm_launch(a, s);
+  else if (int rc = gemm_launch(a, s))
+    return rc;
   return check_launch("gemm_nt_partials");
 }
 

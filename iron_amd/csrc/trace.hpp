@@ -5,7 +5,7 @@
 //                     shared by every XCD), k < kTraceStamps
 // Stamp k is the moment the workgroup's wave 0 passed the kernel's k-th trace
 // point; a point the workgroup never reaches stays as the caller zero-filled
-// it. Kernels on the decode path have a separate traced instance, launched
+// it. The GEMV, decode attention and bf16 GEMM kernels have a separate traced instance, launched
 // only while a buffer is armed (their untraced instance holds no trace code: a
 // clock read at entry measured 0.1 us on the int4 GEMV). In a kernel without
 // one, each trace point is a uniform branch on the trace pointer, and the
@@ -19,7 +19,7 @@
 namespace iron {
 namespace {
 
-enum TraceKernel : unsigned { kTraceGqaDecode = 1, kTraceGemvI4 = 2, kTraceSwigluDecode = 3 };
+enum TraceKernel : unsigned { kTraceGqaDecode = 1, kTraceGemvI4 = 2, kTraceSwigluDecode = 3, kTraceGemm = 4 };
 constexpr int kTraceStamps = 6;
 constexpr int kTraceRecordBytes = 64;
 

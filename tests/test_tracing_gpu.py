@@ -121,3 +121,29 @@ def test_trace_swiglu_one_launch(gpu):
     assert len(recs) == 256 and all(len(r["stamps"]) == 5 and _monotone(r) for r in recs)
     last_publish = max(r["stamps"][2] for r in recs)
     assert all(r["stamps"][3] >= last_publish for r in recs)
+
+
+def test_trace_gemm_cfg5(gpu):
+    """The config 5 prefill GEMM (512 x 2048 x 8192, 128x128 tiles): 256
+    workgroups, six trace points each, output bit-identical untraced."""
+    from iron_amd import _lib
+
+    print("trace: gemm cfg5", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    M, K, N = 512, 2048, 8192
+    A = torch.randn(M, K, device=gpu, generator=g).to(BF16)
+    W = (torch.randn(N, K, device=gpu, generator=g) * 0.02).to(BF16)
+    s = _lib.stream_handle(gpu)
+    buf = tu.new_buffer(1 << 16, gpu)
+    cs = []
+    for traced in (False, True):
+        C = torch.empty(M, N, dtype=BF16, device=gpu)
+        if traced:
+            tu.arm(buf)
+        _lib.call("iron_gemm_bf16_nt", A.data_ptr(), W.data_ptr(), C.data_ptr(), M, N, K, N, 0, 0, 0.0, 0.0, s)
+        torch.cuda.synchronize()
+        cs.append(C)
+    assert _bits_equal(cs[0], cs[1])
+    recs = tu.parse_records(buf)
+    assert len(recs) == 256 and all(r["name"] == "gemm_bf16" for r in recs)
+    assert all(len(r["stamps"]) == 6 and _monotone(r) for r in recs)
