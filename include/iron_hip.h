@@ -57,7 +57,9 @@ int iron_time_next_launch(void* start_event, void* stop_event);
  *   not reach one).
  * A call whose kernel needs more records than `bytes` holds is refused with
  * IRON_EINVAL before it launches; calls without trace points ignore it. The
- * trace is disarmed by that call; NULL disarms. Outputs are unchanged. */
+ * trace is disarmed by that call; NULL disarms. The buffer must stay allocated
+ * until that call's kernels have run (or the trace is disarmed). Outputs are
+ * unchanged. */
 int iron_trace_next_launch(void* buffer, long long bytes);
 
 /* Epilogue codes shared by GEMV and GEMM. GELU_TANH is the tanh approximation

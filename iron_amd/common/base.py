@@ -225,10 +225,19 @@ class HIPOperator(AIEOperatorBase):
 
         def call(*args: torch.Tensor):
             self.validate_args(args)
-            if trace_size > 0:
-                call.trace_buffer = new_buffer(trace_size, args[0].device)
-                arm(call.trace_buffer)
-            self._launch(*args, stream=_lib.stream_handle(args[0].device))
+            stream = _lib.stream_handle(args[0].device)
+            if trace_size <= 0:
+                self._launch(*args, stream=stream)
+                return
+            call.trace_buffer = new_buffer(trace_size, args[0].device)
+            arm(call.trace_buffer)
+            try:
+                self._launch(*args, stream=stream)
+            except BaseException:
+                # a launch that failed before reaching an entry point must not
+                # leave the buffer armed for a later call
+                _lib.call("iron_trace_next_launch", None, 0)
+                raise
 
         call.operator = self
         call.trace_buffer = None

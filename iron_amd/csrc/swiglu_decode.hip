@@ -23,7 +23,9 @@
 // 128) and the exchange pairs (from offset 256). A call tags its pairs with
 // epoch + 1, read by every workgroup at its start; workgroup 0 advances the
 // epoch (skipping the value whose successor is 0) once its gather has seen
-// every pair of the call, i.e. once every workgroup has read the old value.
+// every pair of the call, i.e. once every workgroup has read the old value
+// (not after a give-up, which the caller resolves by zero-filling the
+// workspace).
 // Pairs left by an earlier call carry an older tag and are never accepted.
 //
 // Bounded waits: a gather that does not see its pairs within wait_us, or sees
@@ -207,8 +209,10 @@ __global__ __launch_bounds__(kSwWaves * kWave) void swiglu_decode_i4_kernel(SwAr
   }
   if (!ok && lane == 0) give_up(status, 1u);
   const int failed = __syncthreads_or(!ok);
-  // Every workgroup has read the epoch (each published its pairs after doing so).
-  if (blockIdx.x == 0 && tid == 0) *epoch = (e + 1u == 0xffffffffu) ? 0u : e + 1u;
+  // Once this gather has seen every pair, every workgroup has read the epoch
+  // (each published its pairs after doing so). After a give-up the status word
+  // is set and the caller zero-fills the workspace, epoch included.
+  if (blockIdx.x == 0 && tid == 0 && !failed) *epoch = (e + 1u == 0xffffffffu) ? 0u : e + 1u;
   if (failed) return;
   trace_stamp(a.trace, kTraceSwigluDecode, blockIdx.x, 3);
 
