@@ -291,19 +291,32 @@ struct I4Args {
 // TR: the instance launched while a phase trace is armed (trace.hpp); the
 // others carry no trace code, whose clock read at entry measured 0.1 us of the
 // headline launch.
+// The pointers and the row count that the first loads need come as leading
+// arguments, which the dispatch preloads into SGPRs (the kernarg preload
+// count of this file's build); the rest of I4Args is read from the kernel
+// argument segment while those loads are in flight. With every argument in the
+// struct, no wave could issue a load before its argument fetch returned: the
+// headline 8192 x 2048 launch took 3.97 us that way against 3.42 with the
+// leading arguments preloaded (same outputs). For the same reason the grid
+// size behind the XCD-contiguous row order comes from M, not from the
+// dispatch packet.
 template <int GPL, int R, int KS, bool PAIR, int NM, bool TR>
-__global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
+__global__ __launch_bounds__(256) void gemv_i4_fast(const uint8_t* codes, const uint16_t* scales, const uint16_t* x,
+                                                   const uint8_t* codes2, const uint16_t* scales2,
+                                                   const uint16_t* resid, int M, I4Args a) {
   static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
+  constexpr int kRowsPerBlock = R * 4 / KS;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   // trace points: 0 start, 1 x prepared, 2 row products done
   void* const trace = TR ? a.trace : nullptr;
   unsigned long long t_start = 0;
   if constexpr (TR) t_start = trace_clock();
-  const int tile = xcd_block(a.xcd);
+  const int tile = xcd_tile((M + kRowsPerBlock - 1) / kRowsPerBlock);
   const int rg = wave / KS, kp = wave % KS;
   const int row0 = (tile * (4 / KS) + rg) * R;
-  const bool active = row0 < a.M;  // uniform per row group
-  if (KS == 1 && !active && !a.keys) return;
+  // uniform per row group; an inactive wave does not leave early, since that
+  // test would wait for the keys argument before the first load is issued
+  const bool active = row0 < M;
   constexpr int G = GPL * kWave * KS;                   // groups per row
   constexpr size_t crow = static_cast<size_t>(G) * 16;  // code bytes per row
   const int g0 = kp * GPL * kWave + lane;               // this lane's first group
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
     // wave (measured: SwiGLU pair 4-7% and o_proj 4% faster with it). Issuing
     // x after the weights instead was 7-11% slower.
     uint4 xr[GPL][4];
-    const uint4* xv = reinterpret_cast<const uint4*>(a.x);
+    const uint4* xv = reinterpret_cast<const uint4*>(x);
 #pragma unroll
     for (int j = 0; j < GPL; ++j)
 #pragma unroll
@@ -339,8 +352,8 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
         const int g = g0 + j * kWave;
-        cw[r][j] = ld_stream16(a.codes + row * crow + static_cast<size_t>(g) * 16);
-        if (PAIR) cw2[r][j] = ld_stream16(a.codes2 + row * crow + static_cast<size_t>(g) * 16);
+        cw[r][j] = ld_stream16(codes + row * crow + static_cast<size_t>(g) * 16);
+        if (PAIR) cw2[r][j] = ld_stream16(codes2 + row * crow + static_cast<size_t>(g) * 16);
       }
     }
 #pragma unroll
@@ -349,12 +362,12 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
 #pragma unroll
       for (int j = 0; j < GPL; ++j) {
         const int g = g0 + j * kWave;
-        sc[r][j] = a.scales[row * G + g];
-        if (PAIR) sc2[r][j] = a.scales2[row * G + g];
+        sc[r][j] = scales[row * G + g];
+        if (PAIR) sc2[r][j] = scales2[row * G + g];
       }
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) rres[r] = bf16_to_f32(a.resid ? a.resid[row0 + r] : a.x[0]);  // unconditional load
+    for (int r = 0; r < R; ++r) rres[r] = bf16_to_f32(resid ? resid[row0 + r] : x[0]);  // unconditional load
     __builtin_amdgcn_sched_barrier(0);
     trace_write(trace, kTraceGemvI4, blockIdx.x, 0, t_start);
     if (NM != NORM_NONE) {
@@ -443,14 +456,14 @@ __global__ __launch_bounds__(256) void gemv_i4_fast(I4Args a) {
         t2 *= inv;
       }
       float v = 0.f;
-      if (lane == 0) v = finish_row(a.resid != nullptr, rres[r], a.epi, a.y, row0 + r, t, t2, PAIR);
+      if (lane == 0) v = finish_row(resid != nullptr, rres[r], a.epi, a.y, row0 + r, t, t2, PAIR);
       if (KS == 1 && a.keys) {
         const unsigned long long k = argmax_key(__shfl(v, 0, kWave), row0 + r);
         key = k > key ? k : key;
       }
     }
   }
-  if (KS == 1 && a.keys) publish_key<R>(a.keys, tile, key, (static_cast<size_t>(a.M) + 3) / 4);
+  if (KS == 1 && a.keys) publish_key<R>(a.keys, tile, key, (static_cast<size_t>(M) + 3) / 4);
   advance_epoch(a.epoch);  // last: at the start it would serialise the argument loads
 }
 
@@ -513,11 +526,15 @@ int launch_i4_fast(I4Args a, int norm_mode, hipStream_t s) {
   if (int rc = take_trace("iron_gemv_i4g32", grid.x, &a.trace)) return rc;
   auto go = [&](auto tr) {
     constexpr bool TR = decltype(tr)::value;
+#define IRON_I4_FAST(NM)                                                                                       \
+  IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NM, TR>), grid, block, 0, s, a.codes, a.scales, a.x, a.codes2, \
+              a.scales2, a.resid, a.M, a)
     switch (norm_mode) {
-      case NORM_WEIGHT: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_WEIGHT, TR>), grid, block, 0, s, a); break;
-      case NORM_SCALE: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_SCALE, TR>), grid, block, 0, s, a); break;
-      default: IRON_LAUNCH((gemv_i4_fast<GPL, R, KS, PAIR, NORM_NONE, TR>), grid, block, 0, s, a); break;
+      case NORM_WEIGHT: IRON_I4_FAST(NORM_WEIGHT); break;
+      case NORM_SCALE: IRON_I4_FAST(NORM_SCALE); break;
+      default: IRON_I4_FAST(NORM_NONE); break;
     }
+#undef IRON_I4_FAST
   };
   if (a.trace)
     go(std::true_type{});

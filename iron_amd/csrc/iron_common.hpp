@@ -195,6 +195,14 @@ __device__ __forceinline__ int xcd_block(int enable) {
   return (!enable || (nb & 7)) ? b : (b & 7) * (nb >> 3) + (b >> 3);
 }
 
+// xcd_block(1) for a kernel that knows its grid size nb (== gridDim.x) from its
+// own arguments: gridDim.x is read from the dispatch packet, a scalar load
+// that every address computation behind it would wait for.
+__device__ __forceinline__ int xcd_tile(int nb) {
+  const int b = blockIdx.x;
+  return (nb & 7) ? b : (b & 7) * (nb >> 3) + (b >> 3);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
