@@ -473,12 +473,12 @@ static void gqa_decode_dispatch(const DecodeArgs& a, int n_kv_heads, bool one_la
     DecodeArgs b = a;
     b.nsplit = (a.max_len + 16 * kDecWaves1 - 1) / (16 * kDecWaves1);
     if (long_chunks)
-      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1, TR>), dim3(b.nsplit * n_kv_heads),
-                  dim3(kDecWaves1 * kWave), 0, s, b);
+      IRON_GQA_DECODE_LAUNCH((gqa_decode_kernel<G, true, RES, kDecWaves1, TR>), dim3(b.nsplit * n_kv_heads),
+                             dim3(kDecWaves1 * kWave), s, b);
     else
-      IRON_LAUNCH((gqa_decode_kernel<G, true, RES, 4, TR>), dim3(a.nsplit * n_kv_heads), block, 0, s, a);
+      IRON_GQA_DECODE_LAUNCH((gqa_decode_kernel<G, true, RES, 4, TR>), dim3(a.nsplit * n_kv_heads), block, s, a);
   } else {
-    IRON_LAUNCH((gqa_decode_kernel<G, false, RES, 4, TR>), dim3(a.nsplit, n_kv_heads), block, 0, s, a);
+    IRON_GQA_DECODE_LAUNCH((gqa_decode_kernel<G, false, RES, 4, TR>), dim3(a.nsplit, n_kv_heads), block, s, a);
     IRON_LAUNCH((gqa_combine_kernel<G>), dim3(n_kv_heads * G), dim3(kMergeThreads), 0, s, a);
   }
 }

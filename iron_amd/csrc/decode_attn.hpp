@@ -581,20 +581,47 @@ __device__ void gqa_merge_heads(const DecodeArgs& a, int j, int nact, int tid, c
   }
 }
 
+// The arguments that the position load and the first K/V, q and table loads
+// need come first, as copies of their DecodeArgs fields: the dispatch preloads
+// them into SGPRs (the kernarg preload count of the including file's build),
+// so a workgroup issues the position load without waiting for an argument
+// fetch, and the fetch of the other fields overlaps it.
 template <int G, bool MERGE, bool RES, int NW, bool TR>
-__global__ __launch_bounds__(NW * kWave) void gqa_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(NW * kWave) void gqa_decode_kernel(const int* pos_dev, const uint16_t* k_cache,
+                                                                const uint16_t* v_cache, const float* angles,
+                                                                const uint16_t* q, int pos, int nsplit, int max_len,
+                                                                int angle_rows, DecodeArgs a) {
   int s, j;
   if constexpr (MERGE) {
     const int n = blockIdx.x, t = n / kXcds;
-    j = n % kXcds + kXcds * (t / a.nsplit);
-    s = t % a.nsplit;
+    j = n % kXcds + kXcds * (t / nsplit);
+    s = t % nsplit;
   } else {
     s = blockIdx.x;
     j = blockIdx.y;
   }
-  PlainDecodeIo<G> io{a};
-  gqa_decode_chunk<G, MERGE, RES, NW, PlainDecodeIo<G>, TR>(a, s, j, a.pos_dev ? *a.pos_dev : a.pos, io);
+  DecodeArgs b = a;
+  b.k_cache = const_cast<uint16_t*>(k_cache);
+  b.v_cache = const_cast<uint16_t*>(v_cache);
+  b.angles = angles;
+  b.q = q;
+  b.nsplit = nsplit;
+  b.max_len = max_len;
+  b.angle_rows = angle_rows;
+  const int p = pos_dev ? *pos_dev : pos;
+  // k_new and v_new are fetched here, together with the position: fetched where
+  // the chunk first uses them (after the position checks), they added a
+  // second argument round trip ahead of the K/V loads
+  asm volatile("" ::"s"(b.k_new), "s"(b.v_new));
+  PlainDecodeIo<G> io{b};
+  gqa_decode_chunk<G, MERGE, RES, NW, PlainDecodeIo<G>, TR>(b, s, j, p, io);
 }
+
+// Launch of gqa_decode_kernel with its leading copies taken from `a`.
+#define IRON_GQA_DECODE_LAUNCH(KERNEL, GRID, BLOCK, STREAM, A)                                                  \
+  IRON_LAUNCH(KERNEL, GRID, BLOCK, 0, STREAM, (A).pos_dev, static_cast<const uint16_t*>((A).k_cache),          \
+              static_cast<const uint16_t*>((A).v_cache), (A).angles, (A).q, (A).pos, (A).nsplit, (A).max_len,     \
+              (A).angle_rows, A)
 
 // Merge of the chunk partials, one 1024-thread workgroup per query head
 // (Hkv * G workgroups). Thread -> output dim d of the head and slice q of the
