@@ -50,12 +50,13 @@ HIP_FLAGS = [
 # -fno-honor-nans: max(a, b) of finite scores then needs no NaN-quieting
 # v_max_f32 per operand (finite inputs give identical results).
 # decode_fused.hip runs the same decode attention body, so it takes the same flags.
-# gemv.hip, attention.hip: the dispatch preloads a kernel's leading scalar and
-# pointer arguments into SGPRs (up to 14 SGPRs; a struct argument ends the
-# preloaded run), so the int4 GEMV and the decode attention issue their first
-# loads without waiting for an argument fetch.
+# gemv.hip, attention.hip, llama.hip: the dispatch preloads a kernel's leading
+# scalar and pointer arguments into SGPRs (up to 14 SGPRs; a struct argument
+# ends the preloaded run), so the GEMVs, the decode attention and the token
+# select issue their first loads without waiting for an argument fetch.
 FILE_FLAGS = {
     "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"],
+    "llama.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans", "-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "decode_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
 }

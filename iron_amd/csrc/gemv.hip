@@ -46,7 +46,6 @@ struct GemvArgs {
   int M, K;
   float eps;
   int epi;
-  int xcd;  // 1: XCD-contiguous row order (xcd_block)
   unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
 };
 
@@ -114,20 +113,24 @@ __device__ __forceinline__ void advance_epoch(unsigned* epoch) {
 
 // Fast path: K == 512*U exactly; each lane holds U chunks of W (and W2) in
 // flight. One wave per output row.
+// W, W2, x, the residual and M come as leading arguments, preloaded into SGPRs
+// by the dispatch (as for the int4 fast path), and K is 512 U; an inactive
+// wave does not leave early, since that test would wait for the keys argument.
 template <int U, bool PAIR, int NM>
-__global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
+__global__ __launch_bounds__(256) void gemv_bf16_fast(const uint16_t* W, const uint16_t* W2, const uint16_t* xin,
+                                                     const uint16_t* resid, int M, GemvArgs a) {
+  constexpr int K = 512 * U;
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = xcd_block(a.xcd);
+  const int tile = blockIdx.x;  // round-robin rows (see iron_gemv_bf16)
   const int row = tile * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
-  const bool active = row < a.M;  // uniform per wave
-  if (!active && !a.keys) return;  // without keys the kernel has no block barrier
+  const bool active = row < M;  // uniform per wave
   unsigned long long key = 0;
   if (active) {
-    const uint16_t* x = a.x + static_cast<size_t>(b) * a.K;
-    const size_t roff = (static_cast<size_t>(b) * a.M + row) * static_cast<size_t>(a.K);
-    const uint4* Wr = reinterpret_cast<const uint4*>(a.W + roff) + lane;
-    const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(a.W2 + roff) + lane : nullptr;
+    const uint16_t* x = xin + static_cast<size_t>(b) * K;
+    const size_t roff = (static_cast<size_t>(b) * M + row) * static_cast<size_t>(K);
+    const uint4* Wr = reinterpret_cast<const uint4*>(W + roff) + lane;
+    const uint4* W2r = PAIR ? reinterpret_cast<const uint4*>(W2 + roff) + lane : nullptr;
     const uint4* xv = reinterpret_cast<const uint4*>(x) + lane;
 
     uint4 w[U], w2[U], xc[U];
@@ -141,13 +144,13 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
     // The residual is loaded with the operands, not after the reduction; the
     // load is unconditional (x[0] stands in when there is none) so that no
     // branch makes the compiler wait for every load in flight.
-    const float rv = bf16_to_f32(a.resid ? a.resid[row] : a.x[0]);
+    const float rv = bf16_to_f32(resid ? resid[row] : xin[0]);
     float inv = 1.f;
     if (NM != NORM_NONE) {
       float ss = 0.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) ss = sumsq_chunk(xc[u], ss);
-      inv = inv_rms(wave_sum(ss), a.K, a.eps);
+      inv = inv_rms(wave_sum(ss), K, a.eps);
     }
     if (NM == NORM_WEIGHT) {
       const uint4* nw = reinterpret_cast<const uint4*>(a.norm_w) + lane;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
       acc2 *= inv;
     }
     float v = 0.f;
-    if (lane == 0) v = finish_row(a.resid != nullptr, rv, a.epi, a.y, static_cast<size_t>(b) * a.M + row, acc, acc2, PAIR);
+    if (lane == 0) v = finish_row(resid != nullptr, rv, a.epi, a.y, static_cast<size_t>(b) * M + row, acc, acc2, PAIR);
     if (a.keys) key = argmax_key(__shfl(v, 0, kWave), row);
   }
   if (a.keys) publish_key(a.keys, static_cast<size_t>(b) * gridDim.x + tile, key);
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256) void gemv_bf16_fast(GemvArgs a) {
 template <bool PAIR>
 __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mode) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int tile = xcd_block(a.xcd);
+  const int tile = blockIdx.x;
   const int row = tile * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
   const bool active = row < a.M;
@@ -231,11 +234,14 @@ __global__ __launch_bounds__(256) void gemv_bf16_generic(GemvArgs a, int norm_mo
 
 template <int U, bool PAIR>
 void launch_bf16_fast(const GemvArgs& a, int norm_mode, dim3 grid, hipStream_t s) {
+#define IRON_BF16_FAST(NM) \
+  IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NM>), grid, dim3(256), 0, s, a.W, a.W2, a.x, a.resid, a.M, a)
   switch (norm_mode) {
-    case NORM_WEIGHT: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_WEIGHT>), grid, dim3(256), 0, s, a); break;
-    case NORM_SCALE: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_SCALE>), grid, dim3(256), 0, s, a); break;
-    default: IRON_LAUNCH((gemv_bf16_fast<U, PAIR, NORM_NONE>), grid, dim3(256), 0, s, a); break;
+    case NORM_WEIGHT: IRON_BF16_FAST(NORM_WEIGHT); break;
+    case NORM_SCALE: IRON_BF16_FAST(NORM_SCALE); break;
+    default: IRON_BF16_FAST(NORM_NONE); break;
   }
+#undef IRON_BF16_FAST
 }
 
 template <bool PAIR>
@@ -279,7 +285,6 @@ struct I4Args {
   int epi;
   uint32_t magic;  // 0x43084308 signed two's-complement nibbles, 0x43004300 unsigned
   float offset;    // 136 signed, 128 unsigned
-  int xcd;         // 1: XCD-contiguous row order (xcd_block)
   unsigned* epoch;  // optional: advanced by one (skipping 0) by the first thread of the grid
   void* trace;      // phase trace records (trace.hpp), or null
 };
@@ -297,8 +302,9 @@ struct I4Args {
 // argument segment while those loads are in flight. With every argument in the
 // struct, no wave could issue a load before its argument fetch returned: the
 // headline 8192 x 2048 launch took 3.97 us that way against 3.42 with the
-// leading arguments preloaded (same outputs). For the same reason the grid
-// size behind the XCD-contiguous row order comes from M, not from the
+// leading arguments preloaded (same outputs). Rows are XCD-contiguous
+// (xcd_tile; measured faster for every int4 shape of the decode step), and for
+// the same reason the grid size behind that order comes from M, not from the
 // dispatch packet.
 template <int GPL, int R, int KS, bool PAIR, int NM, bool TR>
 __global__ __launch_bounds__(256) void gemv_i4_fast(const uint8_t* codes, const uint16_t* scales, const uint16_t* x,
@@ -665,8 +671,8 @@ extern "C" int iron_gemv_bf16(const void* W, const void* x, void* y, int M, int 
   IRON_REQUIRE(epilogue >= EPI_NONE && epilogue <= EPI_GELU_SIGMOID, "iron_gemv_bf16: bad epilogue %d",
                epilogue);
   GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x),
-             static_cast<uint16_t*>(y), nullptr, nullptr, nullptr, M, K, 0.f, epilogue,
-             0};  // round-robin rows: the XCD-contiguous order measured slower for bf16 rows
+             static_cast<uint16_t*>(y), nullptr, nullptr, nullptr, M, K, 0.f,
+             epilogue};  // round-robin rows: the XCD-contiguous order measured slower for bf16 rows
   return launch_gemv_bf16<false>(a, NORM_NONE, batches, static_cast<hipStream_t>(stream));
 }
 
@@ -700,8 +706,7 @@ extern "C" int iron_gemv_bf16_fused(const void* W, const void* W2, const void* x
              M,
              K,
              eps,
-             epilogue,
-             0};  // round-robin rows (see iron_gemv_bf16)
+             epilogue};  // round-robin rows (see iron_gemv_bf16)
   hipStream_t s = static_cast<hipStream_t>(stream);
   return W2 ? launch_gemv_bf16<true>(a, norm_mode, 1, s) : launch_gemv_bf16<false>(a, norm_mode, 1, s);
 }
@@ -744,8 +749,7 @@ extern "C" int iron_gemv_i4g32_fused(const void* codes, const void* scales, cons
            eps,
            epilogue,
            is_signed ? 0x43084308u : 0x43004300u,
-           is_signed ? 136.f : 128.f,
-           1};  // XCD-contiguous rows: measured faster for every int4 shape of the decode step
+           is_signed ? 136.f : 128.f};
   hipStream_t s = static_cast<hipStream_t>(stream);
   return codes2 ? launch_gemv_i4<true>(a, norm_mode, s) : launch_gemv_i4<false>(a, norm_mode, s);
 }
@@ -764,12 +768,12 @@ extern "C" int iron_llama_decode_head(const void* W, const void* codes, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (W) {
     GemvArgs a{static_cast<const uint16_t*>(W), nullptr, static_cast<const uint16_t*>(x), static_cast<uint16_t*>(logits),
-               nullptr, nullptr, static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, 0, epoch};
+               nullptr, nullptr, static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, epoch};
     return launch_gemv_bf16<false>(a, NORM_SCALE, 1, s);
   }
   I4Args a{static_cast<const uint8_t*>(codes), static_cast<const uint16_t*>(scales), nullptr, nullptr,
            static_cast<const uint16_t*>(x), static_cast<uint16_t*>(logits), nullptr, nullptr,
-           static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, 0x43084308u, 136.f, 1, epoch};
+           static_cast<unsigned long long*>(argmax_keys), M, K, eps, EPI_NONE, 0x43084308u, 136.f, epoch};
   return launch_gemv_i4<false>(a, NORM_SCALE, s);
 }
 
