@@ -54,9 +54,12 @@ HIP_FLAGS = [
 # scalar and pointer arguments into SGPRs (up to 14 SGPRs; a struct argument
 # ends the preloaded run), so the GEMVs, the decode attention and the token
 # select issue their first loads without waiting for an argument fetch.
+# probe.hip: the floor probes get the same, so that the floors they measure
+# are those of kernels launched like the product's.
 FILE_FLAGS = {
     "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=7"],
     "llama.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "probe.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=3"],
     "attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans", "-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "decode_fused.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
 }
