@@ -18,8 +18,9 @@ LIB = Path(__file__).resolve().parent.parent / "iron_amd" / "libiron_hip.so"
 BUNDLE_MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 
 
-def _sections(elf: bytes) -> dict:
-    """name -> (file offset, size, address) of an ELF64 little-endian file."""
+def _section_headers(elf: bytes) -> list:
+    """(name, file offset, size, address, link, entry size) per section of an
+    ELF64 little-endian file, in section-index order."""
     assert elf[:4] == b"\x7fELF" and elf[4] == 2 and elf[5] == 1
     shoff, = struct.unpack_from("<Q", elf, 0x28)
     shentsize, shnum, shstrndx = struct.unpack_from("<HHH", elf, 0x3A)
@@ -30,7 +31,12 @@ def _sections(elf: bytes) -> dict:
         end = elf.index(b"\0", names_off + o)
         return elf[names_off + o:end].decode()
 
-    return {name(h[0]): (h[4], h[5], h[3], h[1], h[6], h[9]) for h in hdrs}
+    return [(name(h[0]), h[4], h[5], h[3], h[6], h[9]) for h in hdrs]
+
+
+def _sections(elf: bytes) -> dict:
+    """name -> (file offset, size, address, link, entry size)."""
+    return {h[0]: h[1:] for h in _section_headers(elf)}
 
 
 def _code_objects(lib: bytes) -> list[bytes]:
@@ -53,23 +59,22 @@ def _code_objects(lib: bytes) -> list[bytes]:
 
 def _preload_lengths(co: bytes) -> dict:
     """kernel symbol -> kernarg preload length (SGPRs) from its descriptor."""
-    secs = _sections(co)
-    symoff, symsize, _, _, link, entsize = secs[".dynsym"]
+    hdrs = _section_headers(co)
+    secs = {h[0]: h[1:] for h in hdrs}
+    symoff, symsize, _, _, entsize = secs[".dynsym"]
     stroff = secs[".dynstr"][0]
-    by_index = sorted(secs.values(), key=lambda s: s[0])
     out = {}
     for i in range(symsize // entsize):
         st_name, _, _, st_shndx, st_value, _ = struct.unpack_from("<IBBHQQ", co, symoff + i * entsize)
         end = co.index(b"\0", stroff + st_name)
         name = co[stroff + st_name:end].decode()
-        if not name.endswith(".kd"):
-            continue
+        if not name.endswith(".kd") or not 0 < st_shndx < len(hdrs):
+            continue  # defined descriptors only
         # the descriptor's file offset: its address within the section that holds it
-        for off, size, addr, *_ in by_index:
-            if addr <= st_value < addr + size and off:
-                kd = co[off + st_value - addr:off + st_value - addr + 64]
-                out[name[:-3]] = struct.unpack_from("<H", kd, 58)[0] & 0x7F
-                break
+        _, off, size, addr, _, _ = hdrs[st_shndx]
+        assert addr <= st_value and st_value + 64 <= addr + size, name
+        kd = co[off + st_value - addr:off + st_value - addr + 64]
+        out[name[:-3]] = struct.unpack_from("<H", kd, 58)[0] & 0x7F
     return out
 
 
