@@ -16,8 +16,7 @@ empty kernel as a graph node, a pure streaming read of the decode kernels'
 sizes); --mode swiglu config 4's block (bf16, int4 in two launches, int4 in one
 launch); --mode trace per-workgroup phase traces (iron_trace_next_launch) of the
 decode attention, the headline int4 GEMV and the one-launch SwiGLU block, with
-Perfetto JSON under gpurun_out/traces. The modes exist for kernel traces and
-counters.
+Perfetto JSON in TRACE_DIR. The modes exist for kernel traces and counters.
 
 Headline (``value``): BASELINE configs[1], the fused int4-g32 dequant+GEMV at
 batch 1 (W 8192x2048, gate_proj shape), as HBM GB/s of algorithmic bytes
@@ -93,6 +92,8 @@ METRIC = "GEMV HBM GB/s (% of peak); Llama-3.2-1B decode tok/s, 1 MI355X"
 # and the HBM bytes per launch from its FETCH_SIZE + WRITE_SIZE passes (each
 # scaled by the counter's reading for a copy of known size).
 TRACE_PROFILE = "profiles/gemv_i4g32_cfg2_kernel_trace.md"
+# where --mode trace writes its Perfetto JSON: the results folder that a remote run returns
+TRACE_DIR = os.path.join("gpurun_out", "traces")
 PMC_PROFILE = "profiles/gemv_i4g32_cfg2_pmc.md"
 
 
@@ -526,7 +527,7 @@ def _traced(torch, dev, launch, copies, calls, tag):
     """Device phase traces (iron_trace_next_launch) of `calls` calls of
     launch(i, stream), each on rotated (cold) inputs after a warm round: the
     spread of their spans, and the phase summary of the median-span call,
-    whose Perfetto JSON goes to gpurun_out/traces/<tag>.json."""
+    whose Perfetto JSON goes to TRACE_DIR/<tag>.json."""
     from iron_amd import _lib
     from iron_amd.common import tracing_utils as tu
 
@@ -545,7 +546,7 @@ def _traced(torch, dev, launch, copies, calls, tag):
         runs.append((max(v["span_ns"] for v in summ.values()), recs, summ))
     runs.sort(key=lambda r: r[0])
     span, recs, summ = runs[len(runs) // 2]
-    out_dir = Path("gpurun_out") / "traces"
+    out_dir = Path(TRACE_DIR)
     out_dir.mkdir(parents=True, exist_ok=True)
     with open(out_dir / f"{tag}.json", "w") as f:
         json.dump(tu.perfetto_json(recs), f)
