@@ -19,8 +19,12 @@ def _bits_equal(a, b):
     return torch.equal(a.cpu().contiguous().view(torch.int16), b.cpu().contiguous().view(torch.int16))
 
 
+# (2050, 2048) and (1026, 8192) run the fast path with a last workgroup partly
+# past M: its inactive waves do not leave early and must still write nothing
 @pytest.mark.parametrize(
-    "M,K", [(128, 128), (2048, 8192), (8192, 2048), (512, 64), (3072, 2048), (100, 24), (130, 8200)]
+    "M,K",
+    [(128, 128), (2048, 8192), (8192, 2048), (512, 64), (3072, 2048), (100, 24), (130, 8200), (2050, 2048),
+     (1026, 8192)],
 )
 def test_gemv_reference_golden(gpu, M, K):
     from iron_amd.operators import GEMV
@@ -286,7 +290,11 @@ def test_argmax_keys_and_select(gpu, int4, M):
     assert torch.equal(xo.cpu(), table[expect].cpu())
 
 
-@pytest.mark.parametrize("M,K", [(2048, 8192), (96, 8192), (64, 4096), (65, 4096), (512, 2048), (8192, 2048), (40, 1024)])
+# 8194 x 2048 (two rows per wave), 2050 x 2048 (one) and 1022 x 8192 (a row pair per
+# wave, four groups per lane) leave the last workgroup partly past M: its
+# inactive row groups run to the end without loads or stores
+@pytest.mark.parametrize("M,K", [(2048, 8192), (96, 8192), (64, 4096), (65, 4096), (512, 2048), (8192, 2048), (40, 1024),
+                                 (8194, 2048), (2050, 2048), (1022, 8192)])
 @pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("pair", [False, True])
 def test_gemv_int4_fused_modes(gpu, M, K, mode, pair):
@@ -307,7 +315,8 @@ def test_gemv_int4_fused_modes(gpu, M, K, mode, pair):
     resid = torch.randn(M, generator=g).to(BF16)
     c, s = (t.to(gpu) for t in ops.quantize_int4_g32(W))
     c2, s2 = (t.to(gpu) for t in ops.quantize_int4_g32(W2)) if pair else (None, None)
-    y = torch.empty(M, dtype=BF16, device=gpu)
+    y_pad = torch.full((M + 64,), 7.0, dtype=BF16, device=gpu)  # a sentinel tail past the M outputs
+    y = y_pad[:M]
     xd, nwd, rd = x.to(gpu), nw.to(gpu), resid.to(gpu)
     _lib.call("iron_gemv_i4g32_fused", c.data_ptr(), s.data_ptr(), c2.data_ptr() if pair else None,
               s2.data_ptr() if pair else None, xd.data_ptr(), y.data_ptr(), M, K, 1, mode,
@@ -328,6 +337,8 @@ def test_gemv_int4_fused_modes(gpu, M, K, mode, pair):
             t2 = t2 * inv
         t = torch.nn.functional.silu(t) * t2
     ref = t + resid.double()
+    assert torch.all(y_pad[M:].cpu() == 7.0), "a write past the M outputs"
+    y = y.cpu()
     max_abs, rel_l2 = ops.max_abs_rel_l2(y, ref)
     assert rel_l2 <= 1e-2, rel_l2
     bad = ops.within_bf16_ulps(y, ref, n_ulp=2.0, atol=2e-2)
